@@ -1,0 +1,129 @@
+/*
+ * C ABI of the MI355X (gfx950) spec-decode attention hot path.
+ *
+ * Plain pointers and sizes only: every pointer is a device address (HIP), every
+ * `stream` is a hipStream_t passed as void*. Entry points enqueue work on that
+ * stream, never synchronize the host, never allocate device memory (scratch comes
+ * from the caller's `workspace`), and keep launch geometry a function of the
+ * shape arguments only (not of device-resident lengths), so they can be captured
+ * into a hipGraph. All return 0 on success and a non-zero SD_STATUS_* code
+ * otherwise; sd_last_error() describes the last failure on the calling thread.
+ *
+ * Layouts (row-major, element strides):
+ *   KV cache    [num_blocks, block_size, num_kv_heads, head_dim] bf16, one tensor for K and one for V
+ *               (nanovllm/engine/model_runner.py:260-266 per-layer views).
+ *   q / out     [tokens, num_heads, head_dim] bf16, token stride given, head stride = head_dim.
+ *   block table [seqs, table_width] int32, -1 padded; entries past ceil(len / block_size) are never read.
+ */
+#ifndef SD_ATTN_H
+#define SD_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SD_ABI_VERSION 1
+
+#define SD_STATUS_OK 0
+#define SD_STATUS_BAD_ARGUMENT 1
+#define SD_STATUS_UNSUPPORTED 2
+#define SD_STATUS_WORKSPACE_TOO_SMALL 3
+#define SD_STATUS_LAUNCH_FAILED 4
+
+#define SD_DTYPE_BF16 0
+#define SD_DTYPE_F32 1
+
+int sd_abi_version(void);
+const char* sd_last_error(void);
+
+/*
+ * KV-cache scatter. Replaces the Triton store_kvcache_kernel and its wrapper,
+ * nanovllm/layers/attention.py:10-40.
+ * For idx in [0, num_tokens): slot = slot_mapping[idx]; slot == -1 (any negative) skips the row
+ * (graph padding, attention.py:23); otherwise row idx of key / value (num_kv_heads*head_dim contiguous
+ * bf16 elements, row stride key_row_stride / value_row_stride elements) is copied to slot `slot` of
+ * k_cache / v_cache viewed as [num_slots, num_kv_heads*head_dim]. Slots >= num_slots are skipped.
+ */
+int sd_store_kvcache(const void* key, int64_t key_row_stride, const void* value, int64_t value_row_stride,
+                     void* k_cache, void* v_cache, int64_t num_slots, const int32_t* slot_mapping,
+                     int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim, void* stream);
+
+/*
+ * Decode / speculative-verify attention over the paged cache. Replaces
+ * flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=context_lens, block_table=block_tables,
+ * softmax_scale=scale, causal=True), nanovllm/layers/attention.py:71-78.
+ * q holds num_seqs * num_query_tokens tokens (sequence-major). context_lens[b] counts the cached keys
+ * including the sequence's num_query_tokens new ones; query i sees keys 0 .. context_lens[b]-n+i
+ * (bottom-right causal). context_lens[b] == 0 (padding sequence) writes zeros.
+ * Keys are processed in fixed 512-token splits combined in a fixed order, so a row's result does not
+ * depend on num_seqs, num_query_tokens or the other rows (bitwise).
+ */
+size_t sd_paged_decode_workspace_size(int32_t num_seqs, int32_t num_query_tokens, int32_t num_heads,
+                                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                      int32_t table_width);
+int sd_paged_decode(const void* q, int64_t q_token_stride, const void* k_cache, const void* v_cache,
+                    int64_t num_blocks, int32_t block_size, const int32_t* context_lens,
+                    const int32_t* block_tables, int32_t table_width, int32_t num_seqs,
+                    int32_t num_query_tokens, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                    float scale, void* out, int64_t out_token_stride, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/*
+ * Varlen prefill / mixed prefill+decode attention. Replaces
+ * flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+ * softmax_scale=scale, causal=True, block_table=block_tables), nanovllm/layers/attention.py:64-70.
+ * Sequence s has Lq = cu_seqlens_q[s+1]-cu_seqlens_q[s] queries (rows cu_seqlens_q[s].. of q) and
+ * Lk = cu_seqlens_k[s+1]-cu_seqlens_k[s] keys; query i sees keys 0 .. Lk-Lq+i.
+ * With table_width > 0, k / v are the paged caches (k_token_stride = v_token_stride = num_kv_heads*head_dim)
+ * and key j of sequence s is at block block_tables[s*table_width + j/block_size]; with table_width == 0
+ * key j is row cu_seqlens_k[s]+j of the fresh k / v ([total_k, num_kv_heads, head_dim], given token
+ * strides; sequences whose keys would fall outside total_k rows are skipped).
+ * total_q = cu_seqlens_q[num_seqs]; max_seqlen_q / max_seqlen_k bound the per-sequence lengths.
+ */
+size_t sd_varlen_workspace_size(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_k, int32_t num_heads,
+                                int32_t num_kv_heads, int32_t head_dim);
+int sd_varlen_attention(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
+                        const void* v, int64_t v_token_stride, int64_t total_k, int64_t num_blocks, int32_t block_size,
+                        const int32_t* block_tables, int32_t table_width, const int32_t* cu_seqlens_q,
+                        const int32_t* cu_seqlens_k, int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q,
+                        int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                        float scale, void* out, int64_t out_token_stride, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/*
+ * Speculative-decoding verifier. Replaces verify_drafts(logits, draft_token_ids, num_drafts,
+ * temperatures, draft_logits), nanovllm/layers/sampler.py:28-103, with the reference's internal
+ * torch.rand(S, K) and exponential_(1) [S, V] passed in as `uniforms` and `exp_noise`.
+ * logits: [S*(K+1), vocab] rows (row stride in elements), dtype SD_DTYPE_BF16 or SD_DTYPE_F32.
+ * draft_token_ids int64 [S, K]; num_drafts int64 [S]; temperatures fp32 [S] (0 = greedy).
+ * draft_logits: [S*K, vocab] rows or NULL (n-gram: q is one-hot on the guess).
+ * uniforms fp32 [S, K] and exp_noise fp32 [S, vocab] are read only for rows with temperature != 0
+ * (may be NULL when every temperature is 0).
+ * Outputs num_accepted int64 [S] and next_token int64 [S].
+ */
+size_t sd_verify_workspace_size(int32_t num_seqs, int32_t num_draft_slots, int32_t vocab,
+                                int32_t has_draft_logits);
+int sd_verify_drafts(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                     const int64_t* draft_token_ids, const int64_t* num_drafts, const float* temperatures,
+                     const void* draft_logits, int32_t draft_dtype, int64_t draft_row_stride,
+                     const float* uniforms, const float* exp_noise, int32_t num_seqs, int32_t num_draft_slots,
+                     int32_t vocab, int64_t* num_accepted, int64_t* next_token, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/*
+ * Token sampler. Replaces Sampler.forward(logits, temperatures), nanovllm/layers/sampler.py:5-16, with
+ * the internal exponential_(1) noise passed in as exp_noise fp32 [S, vocab] (NULL if all greedy).
+ * Greedy rows (temperature 0) take the first argmax; the others argmax(softmax(l/T) / max(E, 1e-10)).
+ */
+int sd_sample(const void* logits, int32_t logits_dtype, int64_t logits_row_stride, const float* temperatures,
+              const float* exp_noise, int32_t num_seqs, int32_t vocab, int64_t* next_token, void* workspace,
+              size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SD_ATTN_H */

@@ -1,0 +1,52 @@
+// Shared definitions for the spec-decode attention / verify kernels (CDNA4, gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sd {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// Status codes returned by every C-ABI entry point (0 = success).
+enum Status : int {
+  kOk = 0,
+  kBadArgument = 1,
+  kUnsupported = 2,
+  kWorkspaceTooSmall = 3,
+  kLaunchFailed = 4,
+};
+
+// Records a formatted message for sd_last_error(); returns `code` for `return fail(...)` chains.
+int fail(int code, const char* fmt, ...);
+// Checks hipGetLastError() after a launch; returns kOk or kLaunchFailed (message recorded).
+int check_launch(const char* what);
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet (same rounding as torch's bfloat16 cast).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+  return __builtin_bit_cast(float, ((uint32_t)h) << 16);
+}
+
+// Two fp32 -> one dword holding two bf16 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+}
+
+// Compiler + LDS ordering point for wave-private LDS reuse: waits for this wave's outstanding LDS
+// operations and keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_wave_fence() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+}  // namespace sd

@@ -1,0 +1,495 @@
+// Speculative-decoding verifier and token sampler over the full vocabulary (replaces verify_drafts and
+// Sampler.forward, nanovllm/layers/sampler.py:5-103).
+//
+// Four small kernels, all HBM-streaming over [rows, vocab] tables:
+//   1. row_stats      (row, chunk): per 4096-entry chunk of every target row: first argmax of the raw
+//                     logits; for rows with temperature != 0 also max and sum(exp(x - max)) of x = l / T
+//                     (target rows and, when given, draft rows).
+//   2. verify_decide  (seq): merges chunk stats in chunk order (argmax, logsumexp), applies the accept rule
+//                     u * q(d) < p(d) (or top1 == d for greedy rows) to the leading run of real guesses,
+//                     writes num_accepted and, for greedy rows, next_token.
+//   3. verify_resample(seq, chunk): random rows only: per chunk, the first argmax of p / max(E, 1e-10) and
+//                     of residual / max(E, 1e-10) with p = softmax(row a / T), residual = max(p - q, 0)
+//                     (or p with the rejected n-gram guess zeroed), and whether any residual is positive.
+//   4. verify_finish  (seq): merges the chunk candidates in order and picks the token.
+// Every reduction has a fixed order, so results are deterministic; ties resolve to the first index (and a
+// NaN counts as the largest value), as torch.argmax does.
+#include <math.h>
+
+#include "sd_common.h"
+#include "../../include/sd_attn.h"
+
+namespace sd {
+namespace {
+
+constexpr int kChunk = 4096;      // vocabulary entries per workgroup
+constexpr int kThreads = 256;
+
+struct RowStat {                  // per (row, chunk)
+  float max_x;                    // max of l / T over the chunk (random rows)
+  float sum;                      // sum of exp(l / T - max_x) (random rows)
+  float best;                     // raw logit at the chunk's first argmax (target rows)
+  int32_t best_idx;
+};
+
+struct SeqInfo {
+  int32_t a;                      // accepted guesses
+  int32_t random;                 // 1 if temperature != 0
+  int32_t resid_mode;             // 0: sample from p; 1: n-gram (zero the guess if rejected); 2: draft residual
+  int32_t rejected;               // a < num_drafts
+  int32_t guess;                  // guess token of the rejected slot (n-gram), or -1
+  float Ma, Sa;                   // softmax stats of target row a
+  float Md, Sd;                   // softmax stats of the draft row of the rejected slot
+  float pad[3];
+};
+
+struct Cand {                     // per (seq, chunk)
+  float p_val;
+  int32_t p_idx;
+  float r_val;
+  int32_t r_idx;
+  int32_t any_res;
+  int32_t pad[3];
+};
+
+// true if (v, i) should replace (bv, bi) under torch.argmax order: NaN largest, then value, then lower index.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+template <int DT>
+__device__ __forceinline__ float load_logit(const void* base, int64_t idx) {
+  if (DT == SD_DTYPE_F32) return ((const float*)base)[idx];
+  return bf16_bits_to_f32(((const uint16_t*)base)[idx]);
+}
+
+// Block-wide reductions over 256 threads (4 waves) in a fixed order.
+__device__ __forceinline__ float block_max(float v, float* sh) {
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) sh[w] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+}
+
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) sh[w] = v;
+  __syncthreads();
+  return ((sh[0] + sh[1]) + sh[2]) + sh[3];
+}
+
+__device__ __forceinline__ void block_argmax(float& v, int& i, float* shv, int* shi) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int oi = __shfl_xor(i, off);
+    if (better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) {
+    shv[w] = v;
+    shi[w] = i;
+  }
+  __syncthreads();
+  v = shv[0];
+  i = shi[0];
+  for (int k = 1; k < 4; ++k)
+    if (better(shv[k], shi[k], v, i)) {
+      v = shv[k];
+      i = shi[k];
+    }
+}
+
+struct VParams {
+  const void* logits;
+  int64_t logits_stride;
+  const int64_t* drafts;          // [S, K]
+  const int64_t* num_drafts;      // [S]
+  const float* temps;             // [S]
+  const void* draft_logits;       // [S*K] rows or null
+  int64_t draft_stride;
+  const float* uniforms;          // [S, K]
+  const float* noise;             // [S, V]
+  int32_t S, K, V, nchunk;
+  int64_t* out_a;
+  int64_t* out_next;
+  RowStat* stats;                 // [(S*(K+1) + S*K) rows][nchunk]
+  SeqInfo* info;                  // [S]
+  Cand* cand;                     // [S][nchunk]
+};
+
+template <int DT, int DDT>
+__global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
+  __shared__ float shf[4];
+  __shared__ int shi[4];
+  const int row = blockIdx.x;
+  const int chunk = blockIdx.y;
+  const int target_rows = p.S * (p.K + 1);
+  const bool is_target = row < target_rows;
+  const int seq = is_target ? row / (p.K + 1) : (row - target_rows) / p.K;
+  const float T = p.temps[seq];
+  const bool random = T != 0.f;
+  if (!is_target && !random) return;  // draft rows only matter for sampled rows
+  const void* base;
+  if (is_target) {
+    base = DT == SD_DTYPE_F32 ? (const void*)((const float*)p.logits + (int64_t)row * p.logits_stride)
+                              : (const void*)((const uint16_t*)p.logits + (int64_t)row * p.logits_stride);
+  } else {
+    const int64_t dr = row - target_rows;
+    base = DDT == SD_DTYPE_F32 ? (const void*)((const float*)p.draft_logits + dr * p.draft_stride)
+                               : (const void*)((const uint16_t*)p.draft_logits + dr * p.draft_stride);
+  }
+  const int v0 = chunk * kChunk;
+  const int v1 = min(v0 + kChunk, p.V);
+  constexpr int kPer = kChunk / kThreads;  // 16 entries per thread, strided by kThreads
+  float x[kPer];
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int v = v0 + e * kThreads + threadIdx.x;
+    if (v < v1) {
+      const float raw = is_target ? load_logit<DT>(base, v) : load_logit<DDT>(base, v);
+      if (is_target && better(raw, v, bv, bi)) {
+        bv = raw;
+        bi = v;
+      }
+      x[e] = raw / T;
+    } else {
+      x[e] = -INFINITY;
+    }
+  }
+  RowStat st;
+  st.max_x = 0.f;
+  st.sum = 0.f;
+  if (is_target) block_argmax(bv, bi, shf, shi);
+  st.best = bv;
+  st.best_idx = bi;
+  if (random) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) mx = fmaxf(mx, x[e]);
+    mx = block_max(mx, shf);
+    const float m_use = fabsf(mx) == INFINITY ? 0.f : mx;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) s += expf(x[e] - m_use);
+    s = block_sum(s, shf);
+    st.max_x = m_use;
+    st.sum = s;
+  }
+  if (threadIdx.x == 0) p.stats[(int64_t)row * p.nchunk + chunk] = st;
+}
+
+// Merged (max, sum) of a row's chunks, in chunk order: sum = sum_c sum_c * exp(max_c - M).
+__device__ void merge_softmax(const RowStat* st, int nchunk, float* M_out, float* S_out) {
+  float M = -INFINITY;
+  for (int c = 0; c < nchunk; ++c) M = fmaxf(M, st[c].max_x);
+  float s = 0.f;
+  for (int c = 0; c < nchunk; ++c) s += st[c].sum * expf(st[c].max_x - M);
+  *M_out = M;
+  *S_out = s;
+}
+
+template <int DT, int DDT>
+__global__ __launch_bounds__(64) void verify_decide(VParams p) {
+  __shared__ int32_t top1[65];
+  __shared__ float lse[65];
+  __shared__ float dlse[64];
+  const int seq = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int K = p.K;
+  const float T = p.temps[seq];
+  const bool random = T != 0.f;
+  const int target_rows = p.S * (K + 1);
+  for (int j = lane; j <= K; j += 64) {
+    const RowStat* st = p.stats + (int64_t)(seq * (K + 1) + j) * p.nchunk;
+    float bv = st[0].best;
+    int bi = st[0].best_idx;
+    for (int c = 1; c < p.nchunk; ++c)
+      if (better(st[c].best, st[c].best_idx, bv, bi)) {
+        bv = st[c].best;
+        bi = st[c].best_idx;
+      }
+    top1[j] = bi;
+    if (random) {
+      float M, s;
+      merge_softmax(st, p.nchunk, &M, &s);
+      lse[j] = logf(s) + M;
+    }
+  }
+  if (random && p.draft_logits) {
+    for (int j = lane; j < K; j += 64) {
+      const RowStat* st = p.stats + (int64_t)(target_rows + seq * K + j) * p.nchunk;
+      float M, s;
+      merge_softmax(st, p.nchunk, &M, &s);
+      dlse[j] = logf(s) + M;
+    }
+  }
+  __syncthreads();
+  if (lane != 0) return;
+  const int64_t nd = p.num_drafts ? p.num_drafts[seq] : 0;
+  int a = 0;
+  for (int j = 0; j < K; ++j) {
+    const int64_t d = p.drafts[(int64_t)seq * K + j];
+    bool acc = false;
+    if (j < nd && d >= 0 && d < p.V) {
+      if (!random) {
+        acc = top1[j] == d;
+      } else {
+        const float xl = (DT == SD_DTYPE_F32)
+                             ? ((const float*)p.logits)[(int64_t)(seq * (K + 1) + j) * p.logits_stride + d]
+                             : bf16_bits_to_f32(((const uint16_t*)p.logits)[(int64_t)(seq * (K + 1) + j) * p.logits_stride + d]);
+        const float pd = expf(xl / T - lse[j]);
+        float qd = 1.f;
+        if (p.draft_logits) {
+          const int64_t dr = (int64_t)seq * K + j;
+          const float xd = (DDT == SD_DTYPE_F32)
+                               ? ((const float*)p.draft_logits)[dr * p.draft_stride + d]
+                               : bf16_bits_to_f32(((const uint16_t*)p.draft_logits)[dr * p.draft_stride + d]);
+          qd = expf(xd / T - dlse[j]);
+        }
+        const float u = p.uniforms ? p.uniforms[(int64_t)seq * K + j] : 1.f;  // missing uniforms: u = 1
+        acc = u * qd < pd;
+      }
+    }
+    if (!acc) break;
+    ++a;
+  }
+  p.out_a[seq] = a;
+  SeqInfo info{};
+  info.a = a;
+  info.random = random ? 1 : 0;
+  info.guess = -1;
+  if (!random) {
+    p.out_next[seq] = top1[a];
+  } else {
+    const RowStat* st = p.stats + (int64_t)(seq * (K + 1) + a) * p.nchunk;
+    merge_softmax(st, p.nchunk, &info.Ma, &info.Sa);
+    info.rejected = a < nd ? 1 : 0;
+    if (K > 0) {
+      const int j = min(a, K - 1);
+      const int64_t d = p.drafts[(int64_t)seq * K + j];
+      if (p.draft_logits) {
+        info.resid_mode = 2;
+        merge_softmax(p.stats + (int64_t)(target_rows + seq * K + j) * p.nchunk, p.nchunk, &info.Md, &info.Sd);
+      } else {
+        info.resid_mode = 1;
+        info.guess = (d >= 0 && d < p.V) ? (int32_t)d : -1;
+      }
+    }
+  }
+  p.info[seq] = info;
+}
+
+template <int DT, int DDT>
+__global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
+  __shared__ float shf[4];
+  __shared__ int shi[4];
+  const int seq = blockIdx.x;
+  const int chunk = blockIdx.y;
+  const SeqInfo info = p.info[seq];
+  if (!info.random) return;
+  const float T = p.temps[seq];
+  const int K = p.K;
+  const int64_t trow = (int64_t)seq * (K + 1) + info.a;
+  const int64_t drow = (int64_t)seq * K + min(info.a, K - 1);
+  const float* noise = p.noise ? p.noise + (int64_t)seq * p.V : nullptr;  // missing noise: E = 1
+  const int v0 = chunk * kChunk;
+  const int v1 = min(v0 + kChunk, p.V);
+  constexpr int kPer = kChunk / kThreads;
+  float pv = -INFINITY, rv = -INFINITY;
+  int pi = 0x7fffffff, ri = 0x7fffffff;
+  int any_res = 0;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int v = v0 + e * kThreads + threadIdx.x;
+    if (v >= v1) continue;
+    const float l = (DT == SD_DTYPE_F32) ? ((const float*)p.logits)[trow * p.logits_stride + v]
+                                         : bf16_bits_to_f32(((const uint16_t*)p.logits)[trow * p.logits_stride + v]);
+    float prob = expf(l / T - info.Ma) / info.Sa;
+    const float E = noise ? fmaxf(noise[v], 1e-10f) : 1.f;
+    if (info.resid_mode == 1 && info.rejected && v == info.guess) prob = 0.f;
+    const float sp = prob / E;
+    if (better(sp, v, pv, pi)) {
+      pv = sp;
+      pi = v;
+    }
+    if (info.resid_mode == 2) {
+      const float ld = (DDT == SD_DTYPE_F32)
+                           ? ((const float*)p.draft_logits)[drow * p.draft_stride + v]
+                           : bf16_bits_to_f32(((const uint16_t*)p.draft_logits)[drow * p.draft_stride + v]);
+      const float q = expf(ld / T - info.Md) / info.Sd;
+      const float res = fmaxf(prob - q, 0.f);
+      any_res |= res > 0.f;
+      const float sr = res / E;
+      if (better(sr, v, rv, ri)) {
+        rv = sr;
+        ri = v;
+      }
+    }
+  }
+  block_argmax(pv, pi, shf, shi);
+  Cand c{};
+  c.p_val = pv;
+  c.p_idx = pi;
+  if (info.resid_mode == 2) {
+    block_argmax(rv, ri, shf, shi);
+    any_res = __syncthreads_or(any_res);
+  }
+  c.r_val = rv;
+  c.r_idx = ri;
+  c.any_res = any_res;
+  if (threadIdx.x == 0) p.cand[(int64_t)seq * p.nchunk + chunk] = c;
+}
+
+__global__ __launch_bounds__(64) void verify_finish(VParams p) {
+  const int seq = blockIdx.x * 64 + threadIdx.x;
+  if (seq >= p.S) return;
+  const SeqInfo info = p.info[seq];
+  if (!info.random) return;
+  const Cand* c = p.cand + (int64_t)seq * p.nchunk;
+  float pv = c[0].p_val, rv = c[0].r_val;
+  int pi = c[0].p_idx, ri = c[0].r_idx;
+  int any_res = c[0].any_res;
+  for (int k = 1; k < p.nchunk; ++k) {
+    if (better(c[k].p_val, c[k].p_idx, pv, pi)) {
+      pv = c[k].p_val;
+      pi = c[k].p_idx;
+    }
+    if (better(c[k].r_val, c[k].r_idx, rv, ri)) {
+      rv = c[k].r_val;
+      ri = c[k].r_idx;
+    }
+    any_res |= c[k].any_res;
+  }
+  const bool use_res = info.resid_mode == 2 && info.rejected && any_res;
+  p.out_next[seq] = use_res ? ri : pi;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct VLayout {
+  size_t stats, info, cand, total;
+};
+
+VLayout verify_layout(int S, int K, int V, bool draft) {
+  const int nchunk = (V + kChunk - 1) / kChunk;
+  const int64_t rows = (int64_t)S * (K + 1) + (draft ? (int64_t)S * K : 0);
+  VLayout L;
+  L.stats = 0;
+  L.info = align256((size_t)rows * nchunk * sizeof(RowStat));
+  L.cand = align256(L.info + (size_t)S * sizeof(SeqInfo));
+  L.total = align256(L.cand + (size_t)S * nchunk * sizeof(Cand));
+  return L;
+}
+
+template <int DT, int DDT>
+int launch_all(const VParams& p, hipStream_t s, bool draft) {
+  int rc;
+  const int rows = p.S * (p.K + 1) + (draft ? p.S * p.K : 0);
+  hipLaunchKernelGGL((row_stats<DT, DDT>), dim3(rows, p.nchunk), dim3(kThreads), 0, s, p);
+  if ((rc = check_launch("row_stats"))) return rc;
+  hipLaunchKernelGGL((verify_decide<DT, DDT>), dim3(p.S), dim3(64), 0, s, p);
+  if ((rc = check_launch("verify_decide"))) return rc;
+  hipLaunchKernelGGL((verify_resample<DT, DDT>), dim3(p.S, p.nchunk), dim3(kThreads), 0, s, p);
+  if ((rc = check_launch("verify_resample"))) return rc;
+  hipLaunchKernelGGL(verify_finish, dim3((p.S + 63) / 64), dim3(64), 0, s, p);
+  return check_launch("verify_finish");
+}
+
+int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+               const int64_t* drafts, const int64_t* num_drafts, const float* temps, const void* draft_logits,
+               int32_t draft_dtype, int64_t draft_row_stride, const float* uniforms, const float* noise, int32_t S,
+               int32_t K, int32_t V, int64_t* out_a, int64_t* out_next, void* workspace, size_t workspace_bytes,
+               void* stream) {
+  if (S < 0 || K < 0 || K > 63 || V <= 0)
+    return fail(kBadArgument, "%s: bad sizes (seqs %d, draft slots %d (max 63), vocab %d)", who, S, K, V);
+  if (S == 0) return kOk;
+  if (!logits || !temps || !out_next || (K > 0 && (!drafts || !num_drafts)))
+    return fail(kBadArgument, "%s: null pointer", who);
+  if (logits_dtype != SD_DTYPE_BF16 && logits_dtype != SD_DTYPE_F32)
+    return fail(kUnsupported, "%s: logits dtype %d not supported", who, logits_dtype);
+  if (draft_logits && draft_dtype != SD_DTYPE_BF16 && draft_dtype != SD_DTYPE_F32)
+    return fail(kUnsupported, "%s: draft dtype %d not supported", who, draft_dtype);
+  if (logits_row_stride < V || (draft_logits && draft_row_stride < V))
+    return fail(kBadArgument, "%s: row stride smaller than vocab", who);
+  if ((int64_t)S * (K + 1) + (draft_logits ? (int64_t)S * K : 0) > 0x7fffffff || (V + kChunk - 1) / kChunk > 65535)
+    return fail(kUnsupported, "%s: too many rows or vocabulary entries for one launch", who);
+  const bool draft = draft_logits != nullptr && K > 0;
+  const VLayout lay = verify_layout(S, K, V, draft);
+  if (!workspace || workspace_bytes < lay.total)
+    return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
+  VParams p{};
+  p.logits = logits;
+  p.logits_stride = logits_row_stride;
+  p.drafts = drafts;
+  p.num_drafts = num_drafts;
+  p.temps = temps;
+  p.draft_logits = draft ? draft_logits : nullptr;
+  p.draft_stride = draft_row_stride;
+  p.uniforms = uniforms;
+  p.noise = noise;
+  p.S = S;
+  p.K = K;
+  p.V = V;
+  p.nchunk = (V + kChunk - 1) / kChunk;
+  p.out_a = out_a;
+  p.out_next = out_next;
+  p.stats = (RowStat*)((uint8_t*)workspace + lay.stats);
+  p.info = (SeqInfo*)((uint8_t*)workspace + lay.info);
+  p.cand = (Cand*)((uint8_t*)workspace + lay.cand);
+  hipStream_t s = (hipStream_t)stream;
+  const bool lf = logits_dtype == SD_DTYPE_F32;
+  const bool df = draft && draft_dtype == SD_DTYPE_F32;
+  if (lf && df) return launch_all<SD_DTYPE_F32, SD_DTYPE_F32>(p, s, draft);
+  if (lf) return launch_all<SD_DTYPE_F32, SD_DTYPE_BF16>(p, s, draft);
+  if (df) return launch_all<SD_DTYPE_BF16, SD_DTYPE_F32>(p, s, draft);
+  return launch_all<SD_DTYPE_BF16, SD_DTYPE_BF16>(p, s, draft);
+}
+
+}  // namespace
+}  // namespace sd
+
+using namespace sd;
+
+extern "C" size_t sd_verify_workspace_size(int32_t num_seqs, int32_t num_draft_slots, int32_t vocab,
+                                           int32_t has_draft_logits) {
+  if (num_seqs <= 0 || num_draft_slots < 0 || vocab <= 0) return 0;
+  return verify_layout(num_seqs, num_draft_slots, vocab, has_draft_logits && num_draft_slots > 0).total;
+}
+
+extern "C" int sd_verify_drafts(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                                const int64_t* draft_token_ids, const int64_t* num_drafts, const float* temperatures,
+                                const void* draft_logits, int32_t draft_dtype, int64_t draft_row_stride,
+                                const float* uniforms, const float* exp_noise, int32_t num_seqs,
+                                int32_t num_draft_slots, int32_t vocab, int64_t* num_accepted, int64_t* next_token,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (!num_accepted) return fail(kBadArgument, "sd_verify_drafts: null num_accepted");
+  return run_verify("sd_verify_drafts", logits, logits_dtype, logits_row_stride, draft_token_ids, num_drafts,
+                    temperatures, draft_logits, draft_dtype, draft_row_stride, uniforms, exp_noise, num_seqs,
+                    num_draft_slots, vocab, num_accepted, next_token, workspace, workspace_bytes, stream);
+}
+
+extern "C" int sd_sample(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                         const float* temperatures, const float* exp_noise, int32_t num_seqs, int32_t vocab,
+                         int64_t* next_token, void* workspace, size_t workspace_bytes, void* stream) {
+  // K = 0: the accepted count is always 0; it goes to the tail of the workspace, never to the caller.
+  const size_t need = sd_verify_workspace_size(num_seqs, 0, vocab, 0);
+  if (num_seqs > 0 && (!workspace || workspace_bytes < need + (size_t)num_seqs * sizeof(int64_t)))
+    return fail(kWorkspaceTooSmall, "sd_sample: workspace %zu B < %zu B", workspace_bytes,
+                need + (size_t)num_seqs * sizeof(int64_t));
+  int64_t* scratch_a = num_seqs > 0 ? (int64_t*)((uint8_t*)workspace + need) : nullptr;
+  return run_verify("sd_sample", logits, logits_dtype, logits_row_stride, nullptr, nullptr, temperatures, nullptr,
+                    SD_DTYPE_BF16, 0, nullptr, exp_noise, num_seqs, 0, vocab, scratch_a, next_token, workspace,
+                    workspace_bytes, stream);
+}

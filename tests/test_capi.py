@@ -1,0 +1,76 @@
+"""The C-ABI library (CPU only, no kernel launches): it loads, exports every function include/sd_attn.h
+declares, reports its ABI version, sizes workspaces, and rejects bad arguments with a status code and a
+message before touching the GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from nanovllm_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sd_attn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\**\s+\**(sd_[a-z_0-9]+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) == 10, names
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_abi_version(lib):
+    version = int(re.search(r"#define SD_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    assert lib.sd_abi_version() == version
+
+
+def test_workspace_sizes(lib):
+    # headline verify: 64 sequences x 1 group x 8 kv heads x 17 splits x 32 rows x (128 + 2) fp32
+    assert lib.sd_paged_decode_workspace_size(64, 5, 32, 8, 128, 256, 33) >= 64 * 8 * 17 * 32 * 130 * 4
+    assert lib.sd_paged_decode_workspace_size(0, 5, 32, 8, 128, 256, 33) == 0
+    assert lib.sd_varlen_workspace_size(51, 2048, 4096, 32, 8, 128) > 0
+    assert lib.sd_verify_workspace_size(64, 4, 151936, 1) >= (64 * 5 + 64 * 4) * 38 * 16
+
+
+def test_bad_arguments_return_status(lib):
+    rc = lib.sd_store_kvcache(None, 0, None, 0, None, None, 0, None, -1, 8, 128, None)
+    assert rc == 1 and b"bad sizes" in lib.sd_last_error()
+    assert lib.sd_store_kvcache(None, 0, None, 0, None, None, 0, None, 0, 8, 128, None) == 0   # nothing to do
+    rc = lib.sd_paged_decode(None, 4096, None, None, 10, 256, None, None, 4, 2, 5, 32, 8, 64, 0.1, None, 4096,
+                             None, 0, None)
+    assert rc == 2 and b"head_dim 64" in lib.sd_last_error()
+    rc = lib.sd_paged_decode(None, 4096, None, None, 10, 100, None, None, 4, 2, 5, 32, 8, 128, 0.1, None, 4096,
+                             None, 0, None)
+    assert rc == 2 and b"block_size" in lib.sd_last_error()
+    rc = lib.sd_varlen_attention(None, 4096, None, 1024, None, 1024, 0, 0, 0, None, 0, None, None, 1, 10, 10, 10,
+                                 30, 8, 128, 0.1, None, 4096, None, 0, None)
+    assert rc == 1 and b"multiple" in lib.sd_last_error()
+    rc = lib.sd_verify_drafts(None, 0, 10, None, None, None, None, 0, 0, None, None, 2, 70, 10, None, None, None, 0,
+                              None)
+    assert rc == 1
+    ws = ctypes.create_string_buffer(16)
+    rc = lib.sd_verify_drafts(ctypes.addressof(ws), 7, 10, ctypes.addressof(ws), ctypes.addressof(ws),
+                              ctypes.addressof(ws), None, 0, 0, None, None, 2, 1, 10, ctypes.addressof(ws),
+                              ctypes.addressof(ws), ctypes.addressof(ws), 16, None)
+    assert rc == 2 and b"dtype" in lib.sd_last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load()

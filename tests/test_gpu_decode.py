@@ -1,0 +1,139 @@
+"""Decode / speculative-verify attention on the GPU (HIP sd_paged_decode) against the fp32 oracle.
+
+Tolerance (attention output, bf16): max-abs <= 2e-2 and mean-abs <= 2e-3 versus the fp32 oracle.
+Bitwise properties: batch padding (check_padding.py style: B real rows alone == padded to the graph bucket
+with context_len 0 sequences), spec == non-spec rows (a verify row equals the plain decode of the same
+query at the same position), run-to-run repeatability, hipGraph capture at context_len 0 then replay.
+"""
+import random
+
+import pytest
+import torch
+
+from nanovllm_amd.layers.attention import paged_decode_attention
+from oracle import attention as oatt
+from attn_cases import error_stats, paged_cache, queries
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def _check(device, ctx, n, Hq, Hkv, D=128, W=None, seed=0, tail=-1):
+    B = len(ctx)
+    kc, vc, tables = paged_cache(device, ctx, Hkv, D, W=W, seed=seed, tail=tail)
+    q = queries(device, B * n, Hq, D, seed=seed + 100).view(B, n, Hq, D)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+    scale = D ** -0.5
+    out = paged_decode_attention(q, kc, vc, lens, tables, scale)
+    ref = oatt.paged_decode_attention(q.cpu(), kc.cpu(), vc.cpu(), lens.cpu(), tables.cpu(), scale)
+    mx, mean = error_stats(out.view(B, n, Hq, D), ref)
+    print(f"B={B} n={n} Hq={Hq} Hkv={Hkv} ctx[:4]={ctx[:4]}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+    return out
+
+
+def test_config1_qwen3_06b_shapes(device):
+    """16 q / 8 kv heads, block 256, B 4, ctx {300, 512, 777, 1024}, k = 4 (5 causal queries)."""
+    _check(device, [300, 512, 777, 1024], 5, 16, 8)
+
+
+@pytest.mark.parametrize("B", [1, 16, 64])
+@pytest.mark.parametrize("k", [1, 2, 4, 8])
+def test_config3_qwen3_8b_verify(device, B, k):
+    """32 q / 8 kv heads, contexts uniform in [1024, 8192], table width 33 = ceil((8192 + k) / 256)."""
+    rnd = random.Random(B * 100 + k)
+    ctx = [rnd.randint(1024, 8192) for _ in range(B)]
+    _check(device, ctx, k + 1, 32, 8, W=33, seed=B + k)
+
+
+def test_headline_ctx4096(device):
+    _check(device, [4096] * 64, 5, 32, 8, W=33, seed=7)
+
+
+def test_short_and_edge_contexts(device):
+    """Contexts shorter than a tile, exactly at tile / block / split boundaries, and one past them."""
+    ctx = [5, 31, 32, 33, 255, 256, 257, 511, 512, 513, 1023, 1024, 1025, 2047, 2048, 2049]
+    _check(device, ctx, 5, 32, 8, W=9, seed=3)
+    _check(device, ctx, 1, 32, 8, W=9, seed=4)
+    _check(device, [9, 40, 600], 9, 16, 2, seed=5)        # g = 8, n = 9 -> 72 rows: two query groups
+
+
+def test_padding_sequences_write_zeros_and_stale_tables(device):
+    """context_len 0 rows produce zeros; table entries past the used blocks (-1 or stale ids) are never read."""
+    ctx = [700, 0, 1500, 0]
+    B, n, Hq, Hkv, D = 4, 5, 32, 8, 128
+    kc, vc, tables = paged_cache(device, ctx, Hkv, D, W=12, seed=11, tail=10 ** 6)
+    tables[1].fill_(-1)
+    q = queries(device, B * n, Hq, D, seed=12).view(B, n, Hq, D)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+    out = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5).view(B, n, Hq, D)
+    assert torch.equal(out[1], torch.zeros_like(out[1])) and torch.equal(out[3], torch.zeros_like(out[3]))
+    ref = oatt.paged_decode_attention(q.cpu(), kc.cpu(), vc.cpu(), lens.cpu(), tables.cpu(), D ** -0.5)
+    mx, mean = error_stats(out, ref)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
+
+
+def test_batch_padding_invariance_bitwise(device):
+    """Real rows alone vs padded to the graph bucket with empty sequences: bitwise equal (check_padding.py)."""
+    Hq, Hkv, D, W, n = 32, 8, 128, 17, 5
+    for b, p in [(3, 4), (5, 8), (10, 16), (24, 32), (40, 48)]:
+        ctx = [300 + 97 * i for i in range(b)] + [0] * (p - b)
+        kc, vc, tables = paged_cache(device, ctx, Hkv, D, W=W, seed=b)
+        q = queries(device, p * n, Hq, D, seed=b + 1).view(p, n, Hq, D)
+        lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+        alone = paged_decode_attention(q[:b], kc, vc, lens[:b], tables[:b], D ** -0.5)
+        padded = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5)[:b * n]
+        assert torch.equal(alone, padded), (b, p)
+
+
+def test_spec_rows_equal_plain_decode_bitwise(device):
+    """Verify row i (position L - n + i, sees L - n + i + 1 keys) == plain decode (n = 1) of the same query
+    with context L - n + i + 1: the split layout and combine order depend only on the key positions."""
+    Hq, Hkv, D, W = 32, 8, 128, 33
+    ctx = [513, 1024, 1030, 4096, 700, 8000]
+    for n in (2, 5, 9):
+        B = len(ctx)
+        kc, vc, tables = paged_cache(device, ctx, Hkv, D, W=W, seed=n)
+        q = queries(device, B * n, Hq, D, seed=n + 1).view(B, n, Hq, D)
+        lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+        spec = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5).view(B, n, Hq, D)
+        for i in range(n):
+            plain = paged_decode_attention(q[:, i:i + 1].contiguous(), kc, vc, lens - (n - 1 - i), tables, D ** -0.5)
+            assert torch.equal(plain.view(B, Hq, D), spec[:, i]), (n, i)
+
+
+def test_repeatable_bitwise(device):
+    ctx = [random.Random(3).randint(1024, 8192) for _ in range(16)]
+    kc, vc, tables = paged_cache(device, ctx, 8, 128, W=33, seed=21)
+    q = queries(device, 16 * 5, 32, 128, seed=22).view(16, 5, 32, 128)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+    a = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5)
+    b = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5)
+    assert torch.equal(a, b)
+
+
+def test_graph_capture_at_zero_lengths_then_replay(device):
+    """Captured like capture_cudagraph (all context_lens 0, zero block tables), replayed with real metadata
+    copied into the same buffers; every replay equals the eager result bitwise."""
+    Hq, Hkv, D, W, n, B = 32, 8, 128, 33, 5, 16
+    rnd = random.Random(5)
+    ctx_all = [[rnd.randint(1024, 8192) for _ in range(B)] for _ in range(3)]
+    kc, vc, _ = paged_cache(device, [8192] * B, Hkv, D, W=W, seed=31, extra_blocks=64)
+    q = torch.zeros(B, n, Hq, D, dtype=torch.bfloat16, device=device)
+    lens = torch.zeros(B, dtype=torch.int32, device=device)
+    tables = torch.zeros(B, W, dtype=torch.int32, device=device)
+    out = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5)
+    NB = kc.size(0)
+    for it, ctx in enumerate(ctx_all):
+        g = torch.Generator(device=device).manual_seed(40 + it)
+        q.copy_(queries(device, B * n, Hq, D, seed=50 + it).view(B, n, Hq, D))
+        lens.copy_(torch.tensor(ctx, dtype=torch.int32))
+        tables.copy_(torch.randperm(NB, device=device, generator=g)[:B * W].view(B, W).to(torch.int32))
+        graph.replay()
+        eager = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), it

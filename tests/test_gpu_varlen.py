@@ -1,0 +1,118 @@
+"""Varlen prefill and mixed prefill+decode attention on the GPU (HIP sd_varlen_attention) against the
+fp32 oracle (max-abs <= 2e-2, mean-abs <= 2e-3), plus the bitwise identity of a mixed step's decode rows
+with the decode kernel's rows (so greedy tokens do not depend on whether a step was mixed)."""
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from nanovllm_amd.layers.attention import paged_decode_attention, varlen_attention
+from oracle import attention as oatt
+from attn_cases import BLOCK, error_stats, paged_cache, queries
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def _cu(lengths, device):
+    return torch.tensor([0] + np.cumsum(lengths).tolist(), dtype=torch.int32, device=device)
+
+
+def _check(out, ref, what):
+    mx, mean = error_stats(out, ref)
+    print(f"{what}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (what, mx, mean)
+
+
+def test_prefill_fresh_rows_strided(device):
+    """Plain prefill: no block table, k / v are strided views of a fused qkv tensor (row stride 6144)."""
+    Hq, Hkv, D = 32, 8, 128
+    lens = [1, 17, 64, 100, 300, 613]
+    N = sum(lens)
+    g = torch.Generator(device=device).manual_seed(0)
+    qkv = torch.randn(N, (Hq + 2 * Hkv) * D, device=device, generator=g).to(torch.bfloat16)
+    q = qkv[:, :Hq * D].view(N, Hq, D)
+    k = qkv[:, Hq * D:(Hq + Hkv) * D].view(N, Hkv, D)
+    v = qkv[:, (Hq + Hkv) * D:].view(N, Hkv, D)
+    cu = _cu(lens, device)
+    out = varlen_attention(q, k, v, cu, cu, max(lens), max(lens), D ** -0.5)
+    ref = oatt.varlen_attention(q.cpu(), k.cpu(), v.cpu(), cu.cpu(), cu.cpu(), D ** -0.5)
+    _check(out, ref, "prefill fresh")
+
+
+def test_prefix_cache_chunks(device):
+    """Chunked prefill over the paged cache: Lq new rows after Lk - Lq cached keys."""
+    Hq, Hkv, D = 32, 8, 128
+    pairs = [(50, 306), (220, 732), (1, 1000), (5, 600), (256, 256), (129, 1153), (700, 2100)]
+    lq = [a for a, _ in pairs]
+    lk = [b for _, b in pairs]
+    kc, vc, tables = paged_cache(device, lk, Hkv, D, seed=3)
+    q = queries(device, sum(lq), Hq, D, seed=4)
+    cu_q, cu_k = _cu(lq, device), _cu(lk, device)
+    out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
+    ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
+    _check(out, ref, "prefix-cache chunks")
+
+
+def mixed_step(seed, num_decode=48, k=4, num_chunks=3, budget=2048):
+    """A 2048-token-budget mixed step at Qwen3-8B shapes: decode requests (1+k verify rows, context lognormal
+    median 600, max 4096) first, then prefill chunks (length lognormal median 220, 0-512 cached prefix)."""
+    rnd = np.random.default_rng(seed)
+    dec_ctx = np.minimum(np.exp(rnd.normal(math.log(600), 0.6, num_decode)).astype(int) + k + 1, 4096).tolist()
+    left = budget - num_decode * (1 + k)
+    chunks = []
+    for _ in range(num_chunks):
+        L = int(min(max(np.exp(rnd.normal(math.log(220), 0.5)), 16), left))
+        left -= L
+        prefix = int(rnd.integers(0, 513))
+        chunks.append((L, prefix + L))
+    lq = [1 + k] * num_decode + [a for a, _ in chunks]
+    lk = dec_ctx + [b for _, b in chunks]
+    return lq, lk
+
+
+def test_mixed_step_vs_oracle_and_decode_rows_bitwise(device):
+    Hq, Hkv, D, k = 32, 8, 128, 4
+    lq, lk = mixed_step(0)
+    kc, vc, tables = paged_cache(device, lk, Hkv, D, W=math.ceil(max(lk) / BLOCK), seed=5)
+    q = queries(device, sum(lq), Hq, D, seed=6)
+    cu_q, cu_k = _cu(lq, device), _cu(lk, device)
+    out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
+    ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
+    _check(out, ref, f"mixed step ({sum(lq)} query tokens)")
+    nd = 48
+    dec = paged_decode_attention(q[:nd * (1 + k)].view(nd, 1 + k, Hq, D), kc, vc,
+                                 torch.tensor(lk[:nd], dtype=torch.int32, device=device), tables[:nd], D ** -0.5)
+    assert torch.equal(dec, out[:nd * (1 + k)])
+
+
+def test_varlen_edge_lengths(device):
+    """Zero-length queries, keys shorter than queries (rows that see nothing -> zeros), GQA 2 and 8."""
+    D = 128
+    for Hq, Hkv in ((16, 8), (16, 2)):
+        lq = [0, 3, 40, 1, 17, 10]
+        lk = [5, 3, 600, 1, 513, 4]
+        kc, vc, tables = paged_cache(device, lk, Hkv, D, seed=Hq + Hkv)
+        q = queries(device, sum(lq), Hq, D, seed=9)
+        cu_q, cu_k = _cu(lq, device), _cu(lk, device)
+        out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
+        ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
+        _check(out, ref, f"edge lengths Hq={Hq} Hkv={Hkv}")
+
+
+def test_random_varlen_batches(device):
+    rnd = random.Random(11)
+    Hq, Hkv, D = 32, 8, 128
+    for trial in range(3):
+        n = rnd.randint(1, 12)
+        lq = [rnd.choice([1, 5, rnd.randint(1, 300)]) for _ in range(n)]
+        lk = [a + rnd.randint(0, 1500) for a in lq]
+        kc, vc, tables = paged_cache(device, lk, Hkv, D, seed=20 + trial)
+        q = queries(device, sum(lq), Hq, D, seed=30 + trial)
+        cu_q, cu_k = _cu(lq, device), _cu(lk, device)
+        out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
+        ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
+        _check(out, ref, f"random batch {trial}")
