@@ -1,0 +1,229 @@
+"""Benchmark of the MI355X spec-decode attention hot path (one GPU).
+
+Headline (value): speculative-verify paged attention at Qwen3-8B shapes — 32 query / 8 KV heads, head_dim
+128, bf16 KV cache in 256-token blocks, B = 64 sequences, k = 4 guesses (5 causal queries each), context
+4096 — as algorithmic HBM TB/s: the bytes one call must move (every KV byte of every sequence, the queries,
+the outputs, the block-table entries and context lengths) divided by the measured time. One step = one call
+(one layer). Inputs are resident in HBM before the timed region.
+
+Also reported (same JSON line): the KV-cache scatter (2048 rows, 10% padding slots), the rejection sampler
+(S 64, K 4, V 151936, T 0 and T 1 with draft logits) and a 2048-token mixed prefill+decode attention step
+over 36 layers (tok/s), plus a CPU baseline: the oracle (PyTorch CPU restatement) on a bounded sample of
+the headline workload.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "nano-vllm-spec-decode_amd"), os.path.join(ROOT, "tests")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+HQ, HKV, D, BLOCK = 32, 8, 128, 256
+
+
+def decode_bytes(ctx, n):
+    """Algorithmic bytes of one verify-attention call: K and V of every visible key (Hkv*D*2 B each), the
+    queries and outputs (Hq*D*2 B per row each), block-table entries and the context length."""
+    per_key = 2 * HKV * D * 2
+    per_row = 2 * HQ * D * 2
+    return sum(per_key * c + per_row * n + 4 * math.ceil(c / BLOCK) + 4 for c in ctx)
+
+
+def timed(fn, steps, warmup):
+    """Runs fn warmup times, then `steps` times between two synchronizations; returns (seconds per step,
+    per-call event durations in seconds) measured with events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    ev = [s.elapsed_time(e) / 1e3 for s, e in zip(starts, ends)]
+    return wall, ev
+
+
+def bench_verify_attention(dev, steps, warmup, B=64, k=4, ctx_len=4096, W=33):
+    import torch
+    from attn_cases import paged_cache, queries
+    from nanovllm_amd.layers.attention import paged_decode_attention
+    n = k + 1
+    ctx = [ctx_len] * B
+    kc, vc, tables = paged_cache(dev, ctx, HKV, D, W=W, seed=0)
+    q = queries(dev, B * n, HQ, D, seed=1).view(B, n, HQ, D)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    out = torch.empty(B * n, HQ, D, dtype=torch.bfloat16, device=dev)
+    fn = lambda: paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5, out=out)
+    wall, ev = timed(fn, steps, warmup)
+    nbytes = decode_bytes(ctx, n)
+    return dict(bytes=nbytes, wall_s=wall, event_s=sum(ev) / len(ev), inputs=(q, kc, vc, lens, tables))
+
+
+def bench_store(dev, steps, warmup, N=2048, NB=4096):
+    import torch
+    from nanovllm_amd.layers.attention import store_kvcache
+    g = torch.Generator(device=dev).manual_seed(3)
+    key = torch.randn(N, HKV, D, device=dev, generator=g).to(torch.bfloat16)
+    value = torch.randn(N, HKV, D, device=dev, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(NB * BLOCK, device=dev, generator=g)[:N].to(torch.int32)
+    npad = N // 10
+    slots[torch.randperm(N, device=dev, generator=g)[:npad]] = -1
+    kc = torch.zeros(NB, BLOCK, HKV, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    wall, ev = timed(lambda: store_kvcache(key, value, kc, vc, slots), steps, warmup)
+    nbytes = (N - npad) * 4 * HKV * D * 2 + 4 * N
+    t = sum(ev) / len(ev)
+    return dict(us=t * 1e6, GBs=nbytes / t / 1e9, bytes=nbytes)
+
+
+def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
+    import torch
+    from nanovllm_amd.layers.sampler import verify_drafts
+    g = torch.Generator(device=dev).manual_seed(4)
+    logits = torch.randn(S * (K + 1), V, device=dev, generator=g) * 3
+    dlog = torch.randn(S, K, V, device=dev, generator=g) * 3
+    drafts = dlog.argmax(-1)
+    nd = torch.full((S,), K, device=dev)
+    u = torch.rand(S, K, device=dev, generator=g)
+    e = torch.empty(S, V, device=dev).exponential_(1, generator=g)
+    res = {}
+    for T, with_draft in ((0.0, False), (1.0, True)):
+        temps = torch.full((S,), T, device=dev)
+        dl = dlog if with_draft else None
+        wall, ev = timed(lambda: verify_drafts(logits, drafts, nd, temps, dl, uniforms=u, exp_noise=e), steps, warmup)
+        nbytes = S * (K + 1) * V * 4 + ((S * K * V * 4 + 2 * S * V * 4 + S * V * 4) if T else 0)
+        t = sum(ev) / len(ev)
+        res[f"T{int(T)}"] = dict(us=t * 1e6, GBs=nbytes / t / 1e9, bytes=nbytes)
+    return res
+
+
+def bench_mixed_attention(dev, steps, warmup, layers=36):
+    """Attention phase of a 2048-token-budget mixed step: per layer, store this step's KV then varlen paged
+    attention over 48 decode sequences (k = 4) and 3 prefill chunks (config-5 lengths)."""
+    import numpy as np
+    import torch
+    from attn_cases import paged_cache, queries
+    from nanovllm_amd.layers.attention import store_kvcache, varlen_attention
+    from test_gpu_varlen import mixed_step
+    lq, lk = mixed_step(0)
+    W = math.ceil(max(lk) / BLOCK)
+    kc, vc, tables = paged_cache(dev, lk, HKV, D, W=W, seed=5)
+    caches = [(kc, vc)] + [(torch.empty_like(kc).copy_(kc), torch.empty_like(vc).copy_(vc)) for _ in range(layers - 1)]
+    Nq = sum(lq)
+    q = queries(dev, Nq, HQ, D, seed=6)
+    knew = queries(dev, Nq, HKV, D, seed=7)
+    vnew = queries(dev, Nq, HKV, D, seed=8)
+    tb = tables.cpu()
+    slots = []
+    for s, (a, b) in enumerate(zip(lq, lk)):
+        slots += [int(tb[s, p // BLOCK]) * BLOCK + p % BLOCK for p in range(b - a, b)]
+    slots = torch.tensor(slots, dtype=torch.int32, device=dev)
+    cu_q = torch.tensor([0] + np.cumsum(lq).tolist(), dtype=torch.int32, device=dev)
+    cu_k = torch.tensor([0] + np.cumsum(lk).tolist(), dtype=torch.int32, device=dev)
+    out = torch.empty(Nq, HQ, D, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        for kcl, vcl in caches:
+            store_kvcache(knew, vnew, kcl, vcl, slots)
+            varlen_attention(q, kcl, vcl, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables, out=out)
+
+    wall, ev = timed(step, steps, warmup)
+    t = sum(ev) / len(ev)
+    nd = 48
+    flops = sum(4 * HQ * D * (a * (b - a) + a * (a + 1) / 2) for a, b in zip(lq[nd:], lk[nd:]))
+    dec_bytes = decode_bytes(lk[:nd], 5)
+    return dict(ms=t * 1e3, tok_s=Nq / t, query_tokens=Nq, decode_seqs=nd, prefill_chunks=len(lq) - nd,
+                prefill_flops_per_layer=flops, decode_bytes_per_layer=dec_bytes)
+
+
+def cpu_baseline(inputs, sample_seqs=2):
+    """The oracle (fp32 PyTorch CPU restatement of the reference semantics) on `sample_seqs` of the headline
+    sequences, all host threads; returns GB/s of algorithmic bytes."""
+    import torch
+    from oracle import attention as oatt
+    q, kc, vc, lens, tables = inputs
+    torch.set_num_threads(min(16, os.cpu_count() or 1))   # the GPU box grants 16 host cores per GPU
+    qs = q[:sample_seqs].cpu()
+    ls = lens[:sample_seqs].cpu()
+    ts = tables[:sample_seqs].cpu()
+    used = sorted({int(b) for b in ts.flatten().tolist() if b >= 0})
+    remap = {b: i for i, b in enumerate(used)}
+    kcs = kc[used].cpu()
+    vcs = vc[used].cpu()
+    ts = ts.clone().apply_(lambda b: remap.get(b, -1))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oatt.paged_decode_attention(qs, kcs, vcs, ls, ts, D ** -0.5)
+        times.append(time.perf_counter() - t0)
+    t = min(times)
+    nbytes = decode_bytes(ls.tolist(), q.size(1))
+    return dict(value=nbytes / t / 1e9, unit="GB/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{sample_seqs} of the 64 sequences (ctx 4096, k=4), oracle paged_decode_attention, "
+                       f"min of 3 runs ({t * 1e3:.0f} ms)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--skip-extras", action="store_true", help="headline only (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the hot path shards by sequence or "
+              "KV head with no cross-GPU exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    head = bench_verify_attention(dev, args.steps, args.warmup)
+    t = head["event_s"]
+    achieved = head["bytes"] / t / 1e9
+    value_tbs = head["bytes"] / head["wall_s"] / 1e12
+    result = {
+        "metric": "spec-verify attn TB/s (% HBM peak) Qwen3-8B k=4 B=64; mixed-step tok/s",
+        "value": round(value_tbs, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["wall_s"] * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) bf16 KV cache and queries, randomly permuted block tables)",
+        "config": {"workload": "spec-verify paged attention, Qwen3-8B shapes (32 q / 8 kv heads, head_dim 128), "
+                               "B=64, k=4 (5 causal queries), ctx 4096, block 256, table width 33",
+                   "batch": 64, "k": 4, "context": 4096, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "attn_fwd + attn_combine (one sd_paged_decode call)",
+                     "bytes_per_launch": head["bytes"], "us_per_launch": round(t * 1e6, 2)},
+    }
+    if not args.skip_extras:
+        result["kv_store"] = bench_store(dev, args.steps, args.warmup)
+        result["verify_sampler"] = bench_sampler(dev, max(10, args.steps // 2), args.warmup)
+        mixed = bench_mixed_attention(dev, max(5, args.steps // 10), 2)
+        result["mixed_step_attention"] = mixed
+        result["cpu_baseline"] = cpu_baseline(head["inputs"])
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

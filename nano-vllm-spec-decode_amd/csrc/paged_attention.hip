@@ -6,20 +6,25 @@
 //   * query group: P consecutive query positions of one sequence; with g = Hq/Hkv heads sharing the KV
 //     head, the group holds P*g "rows" (row r = position r/g, head r%g) — GQA head-group sharing: the
 //     KV stream is read once for all g query heads.
-//   * key split: a fixed 512-token range [512*s, 512*(s+1)) of the keys. Split boundaries never depend on
-//     batch size, query count or context length, and partial results are merged in a fixed order, so a
-//     row's output is bitwise independent of the batch it runs in (decode vs verify vs mixed).
-// A 256-thread workgroup (4 waves) handles one item. Each wave streams 32-key tiles j = first + wave,
-// first + wave + 4, ... : 16-byte coalesced global loads into registers (the next tile is in flight
-// while the current one is computed), a wave-private LDS stage (rows padded to 272 B so both the K
-// reads and the transposed V reads below are bank-conflict free), then bf16 MFMA 32x32x16:
-//   S^T[32 keys x 32 rows] = K[32 x 128] . Q^T         (A = K from LDS, B = Q in registers)
-//   O^T[128 d x 32 rows]  += V^T[128 x 32] . P^T        (A = V^T gathered from LDS, B = P in registers)
-// S^T's accumulator layout gives each lane one row and 16 keys, so the online softmax needs one
-// cross-lane exchange (lane ^ 32) per reduction, and P feeds the second MFMA straight from registers
-// (the key order inside each 16-key k-step is permuted identically for P and V^T). The four waves'
-// (max, sum, O) are merged in LDS in wave order; a split that is the sequence's only one writes bf16
-// output directly, otherwise fp32 partials go to the workspace and attn_combine merges splits in order.
+//   * key split: a fixed 512-key range [512*s, 512*(s+1)). Split boundaries never depend on batch size,
+//     query count or context length, and partial results are merged in a fixed order, so a row's output
+//     is bitwise independent of the batch it runs in (decode vs verify vs mixed).
+// A 256-thread workgroup (4 waves) handles one item; wave w streams the 32-key tiles w, w+4, w+8, ... of
+// the split with bf16 MFMA 16x16x32 (rows in 16-row tiles, RT of them):
+//   S^T[16 keys x 16 rows] = K[16 x 128] . Q^T      A = K straight from HBM into registers (16 B per
+//                                                    lane, 64 contiguous bytes per key row per load),
+//                                                    B = Q in registers for the whole split
+//   O^T[16 d x 16 rows]   += V^T[16 x 32] . P^T      A = V^T read transposed from LDS with
+//                                                    ds_read_b64_tr_b16, B = P straight from S^T's
+//                                                    accumulators (the key order inside the 32-key
+//                                                    k-step is permuted identically for P and V^T)
+// V reaches LDS by global_load_lds_dwordx4 (no register staging): each lane fetches the 16-byte chunk
+// that lands, XOR-swizzled, in its own LDS slot, so the transposed reads are bank-conflict free. The next
+// tile's K (registers) and V (LDS) loads are issued right after the current tile's V^T is read, so
+// 16 KB per wave stay in flight while the MFMAs and the online softmax run; at <= 256 VGPRs two
+// workgroups share a CU. The four waves' (max, sum, O) are merged in LDS in wave order; a split that is
+// its item's only one writes bf16 output directly, otherwise fp32 partials go to the workspace and
+// attn_combine merges the splits in order.
 #include <math.h>
 
 #include "sd_common.h"
@@ -32,11 +37,15 @@ constexpr int kD = 128;                        // head_dim (Qwen3)
 constexpr int kTile = 32;                      // keys per wave step
 constexpr int kWaves = 4;                      // waves per workgroup
 constexpr int kSplit = 512;                    // keys per split
-constexpr int kLdsRow = 272;                   // bytes per staged key row: 256 + 16 pad
-constexpr int kLdsTensor = kTile * kLdsRow;    // one 32-key tile of K (or V)
-constexpr int kLdsWave = 2 * kLdsTensor;       // K tile then V tile
-constexpr int kLdsBytes = kWaves * kLdsWave;   // 69,632 B: two workgroups fit a CU's 160 KB
+constexpr int kVBuf = kTile * kD * 2;          // one 32-key V tile in LDS: 8 KB per wave
 constexpr int kObRow = kD + 4;                 // fp32 row stride of the cross-wave O buffer (bank padding)
+constexpr int kMaxRows = 64;                   // 16-row tiles: at most 4
+constexpr int kMergeBytes = 2048 + kMaxRows * kObRow * 4;
+constexpr int kLdsBytes = kMergeBytes > kWaves * kVBuf ? kMergeBytes : kWaves * kVBuf;
+
+#define SD_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
+#define SD_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 struct Params {
   const uint16_t* q;
@@ -108,8 +117,15 @@ __device__ __forceinline__ Item describe(const Params& p, int item) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <int MT, bool kVarlen, bool kPaged>
-__global__ __launch_bounds__(kWaves * kWave) void attn_fwd(Params p) {
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Waits for every outstanding vector-memory load of this wave (including loads into LDS).
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int RT, bool kVarlen, bool kPaged>
+__global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
 
   const int split = blockIdx.x;
@@ -120,10 +136,10 @@ __global__ __launch_bounds__(kWaves * kWave) void attn_fwd(Params p) {
   const int nsplit_act = (it.kmax + kSplit - 1) / kSplit;
   const int rows = it.np * p.g;
   const int tid = threadIdx.x;
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
-  const int r = lane % 32;   // row (within a 32-row tile) owned by this lane
-  const int hh = lane / 32;  // which half of the k / key sub-blocks this lane holds
+  const int r16 = lane % 16;  // row (S^T / O^T column) or key (K operand row) owned by this lane
+  const int grp = lane / 16;  // 16-lane group: which 8 k-elements / 4 accumulator rows
 
   if (it.kmax <= 0) {  // no row sees any key (e.g. context_len 0 padding): zeros, written once
     if (split != 0) return;
@@ -138,224 +154,237 @@ __global__ __launch_bounds__(kWaves * kWave) void attn_fwd(Params p) {
   const int kbeg = split * kSplit;
   const int kend = min(kbeg + kSplit, it.kmax);
 
-  // Per-row visible-key limit inside this split (bottom-right causal: query i sees Lk - Lq + i + 1 keys).
-  int lim[MT];
-  bf16x8 qv[MT][8];
+  // Per-row visible-key limit inside this split (bottom-right causal: query i sees Lk - Lq + i + 1 keys)
+  // and the Q operand (B of S^T): lane holds row 16*rt + r16, d = 32*ks + 8*grp + e.
+  int lim[RT];
+  bf16x8 qv[RT][4];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int row = mt * 32 + r;
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = rt * 16 + r16;
     if (row < rows) {
       const int i = it.p0 + row / p.g;
       const int hq = h * p.g + row % p.g;
-      lim[mt] = min(max(it.Lk - it.Lq + i + 1, 0), kend);
-      const uint16_t* qp = p.q + (int64_t)(it.q_start + i) * p.q_stride + hq * kD + 64 * hh;
+      lim[rt] = min(max(it.Lk - it.Lq + i + 1, 0), kend);
+      const uint16_t* qp = p.q + (int64_t)(it.q_start + i) * p.q_stride + hq * kD + 8 * grp;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) qv[mt][s] = *(const bf16x8*)(qp + 8 * s);
+      for (int ks = 0; ks < 4; ++ks) qv[rt][ks] = *(const bf16x8*)(qp + 32 * ks);
     } else {
-      lim[mt] = kend;  // padding row: Q = 0 keeps its scores finite; never written
+      lim[rt] = kend;  // padding row: Q = 0 keeps its scores finite; never written
 #pragma unroll
-      for (int s = 0; s < 8; ++s) qv[mt][s] = bf16x8{};
+      for (int ks = 0; ks < 4; ++ks) qv[rt][ks] = bf16x8{};
     }
   }
 
-  float m[MT], l[MT];
-  f32x16 o[MT][4];
+  float m[RT], l[RT];
+  f32x4 o[8][RT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    m[mt] = -INFINITY;
-    l[mt] = 0.f;
+  for (int rt = 0; rt < RT; ++rt) {
+    m[rt] = -INFINITY;
+    l[rt] = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[mt][dt] = f32x16{};
+    for (int dt = 0; dt < 8; ++dt) o[dt][rt] = f32x4{};
   }
 
-  uint8_t* kl = lds + wave * kLdsWave;
-  uint8_t* vl = kl + kLdsTensor;
-  // Staging layout: load q covers keys 4q .. 4q+3, 16 lanes per key row, 16 B per lane.
-  const int st_key = lane / 16;
-  const int st_chunk = lane % 16;
-  u32x4 sk[8], sv[8];
+  uint8_t* vbuf = lds + wave * kVBuf;
+  // V fill (global_load_lds): load q puts keys 4q .. 4q+3 at bytes 1024*q + 16*lane, i.e. key
+  // t = 4q + lane/16 in slot s = lane%16, holding chunk s ^ 2*(t%8) (16-byte chunks, 8 d each).
+  const int vf_key = lane / 16;
+  const int vf_slot = lane % 16;
+  // V^T reads (ds_read_b64_tr_b16): source lane reads 4 d of key tl (+16 for the second half) at
+  // d = 16*dt + 4*(lane%4): chunk 2*dt + (lane%4)/2, byte 8*(lane%2) inside it.
+  const int tl = 4 * grp + r16 / 4;
+  uint32_t vt_off[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+    vt_off[dt] = tl * 256 + 8 * (lane % 2) + 16 * (((2 * dt + (lane % 4) / 2) ^ (2 * (tl % 8))));
 
-  auto load_tile = [&](int jt) {
+  // Tile addressing: K / V base of tile jt (keys past the split's end read the tile's first key instead:
+  // finite data, masked out in the softmax). An invalid block id (bad table) reads zeros, never faults.
+  struct TileSrc {
+    const uint16_t* kb;
+    const uint16_t* vb;
+    int nvalid;
+    bool ok;
+  };
+  auto tile_src = [&](int jt) {
+    TileSrc ts;
     const int t0 = jt * kTile;
-    const uint16_t* kb = nullptr;
-    const uint16_t* vb = nullptr;
-    int nvalid = min(kTile, kend - t0);
+    ts.nvalid = min(kTile, kend - t0);
+    ts.ok = true;
     if (kPaged) {
       const int bi = t0 / p.block_size;
       const int blk = bi < p.table_width ? p.block_tables[(int64_t)it.seq * p.table_width + bi] : -1;
-      if (blk < 0 || blk >= p.num_blocks) {
-        nvalid = 0;  // invalid block id reads as zeros instead of faulting
-      } else {
-        const int64_t slot0 = (int64_t)blk * p.block_size + t0 % p.block_size;
-        kb = p.k + slot0 * p.k_stride + h * kD;
-        vb = p.v + slot0 * p.v_stride + h * kD;
-      }
+      ts.ok = blk >= 0 && blk < p.num_blocks;
+      const int64_t slot0 = (int64_t)(ts.ok ? blk : 0) * p.block_size + t0 % p.block_size;
+      ts.kb = p.k + slot0 * p.k_stride + h * kD;
+      ts.vb = p.v + slot0 * p.v_stride + h * kD;
     } else {
       const int64_t row0 = (int64_t)p.cu_k[it.seq] + t0;
-      kb = p.k + row0 * p.k_stride + h * kD;
-      vb = p.v + row0 * p.v_stride + h * kD;
+      ts.kb = p.k + row0 * p.k_stride + h * kD;
+      ts.vb = p.v + row0 * p.v_stride + h * kD;
+    }
+    return ts;
+  };
+  // K of a tile into registers (A of S^T): key 16*kt + r16, d = 32*ks + 8*grp + e.
+  auto load_k = [&](const TileSrc& ts, bf16x8 (&kr)[2][4]) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int tt = 16 * kt + r16;
+      const uint16_t* src = ts.kb + (int64_t)(tt < ts.nvalid ? tt : 0) * p.k_stride + 8 * grp;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kr[kt][ks] = ts.ok ? *(const bf16x8*)(src + 32 * ks) : bf16x8{};
+    }
+  };
+  // V of a tile into this wave's LDS buffer (global_load_lds, 1 KB per instruction).
+  auto load_v = [&](const TileSrc& ts) {
+    if (!ts.ok) {
+      for (int e = lane; e < kVBuf / 16; e += kWave) *(u32x4*)(vbuf + 16 * e) = u32x4{0, 0, 0, 0};
+      return;
     }
 #pragma unroll
     for (int qd = 0; qd < 8; ++qd) {
-      const int tt = 4 * qd + st_key;
-      if (tt < nvalid) {
-        sk[qd] = *(const u32x4*)(kb + (int64_t)tt * p.k_stride + st_chunk * 8);
-        sv[qd] = *(const u32x4*)(vb + (int64_t)tt * p.v_stride + st_chunk * 8);
-      } else {
-        sk[qd] = u32x4{0, 0, 0, 0};
-        sv[qd] = u32x4{0, 0, 0, 0};
-      }
+      const int t = 4 * qd + vf_key;
+      const int chunk = vf_slot ^ (2 * (t % 8));
+      const uint16_t* src = ts.vb + (int64_t)(t < ts.nvalid ? t : 0) * p.v_stride + 8 * chunk;
+      __builtin_amdgcn_global_load_lds(SD_GPTR(src), SD_LPTR(vbuf + 1024 * qd), 16, 0, 0);
     }
   };
 
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int qd = 0; qd < 8; ++qd) {
-      const int off = (4 * qd + st_key) * kLdsRow + st_chunk * 16;
-      *(u32x4*)(kl + off) = sk[qd];
-      *(u32x4*)(vl + off) = sv[qd];
-    }
-  };
-
-  // K operand (A of S^T): lane holds key r, d = 64*hh + 8*ks + e for k-step ks.
-  const uint8_t* k_rd = kl + r * kLdsRow + hh * 128;
-  // V^T operand (A of O^T): lane holds d = 32*dt + r, keys 16*s2 + 4*hh + (e%4) + 8*(e/4).
-  const uint8_t* v_rd = vl + (4 * hh) * kLdsRow + r * 2;
-
-  auto compute_tile = [&](int jt) {
+  // One tile: S^T from the K registers, then (registers free) the next tile's K loads, then the online
+  // softmax and O^T += V^T P^T.
+  auto compute = [&](int jt, bf16x8 (&kr)[2][4], const bf16x8 (&vt)[8], bool has_next, const TileSrc& next) {
     const int t0 = jt * kTile;
-    f32x16 s[MT];
+    f32x4 s[2][RT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) s[mt] = f32x16{};
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 a = *(const bf16x8*)(k_rd + ks * 16);
+      for (int rt = 0; rt < RT; ++rt) {
+        f32x4 acc = f32x4{};
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qv[mt][ks], s[mt], 0, 0, 0);
-    }
-
-    bf16x8 pb[MT][2];
+        for (int ks = 0; ks < 4; ++ks) acc = mfma16(kr[kt][ks], qv[rt][ks], acc);
+        s[kt][rt] = acc;
+      }
+    if (has_next) load_k(next, kr);
+    bf16x8 pb[RT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float x[16];
+    for (int rt = 0; rt < RT; ++rt) {
+      float x[8];
       float mx = -INFINITY;
 #pragma unroll
-      for (int idx = 0; idx < 16; ++idx) {
-        const int tok = t0 + 8 * (idx / 4) + 4 * hh + (idx % 4);
-        x[idx] = tok < lim[mt] ? s[mt][idx] * p.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, x[idx]);
+      for (int e = 0; e < 8; ++e) {
+        const int tok = t0 + 16 * (e / 4) + 4 * grp + (e % 4);
+        x[e] = tok < lim[rt] ? s[e / 4][rt][e % 4] * p.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, x[e]);
       }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m[mt], mx);
+      const float m_new = fmaxf(m[rt], mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2_fast(m[mt] - m_use);
+      const float alpha = exp2_fast(m[rt] - m_use);
       float sum = 0.f;
 #pragma unroll
-      for (int idx = 0; idx < 16; ++idx) {
-        x[idx] = exp2_fast(x[idx] - m_use);
-        sum += x[idx];
+      for (int e = 0; e < 8; ++e) {
+        x[e] = exp2_fast(x[e] - m_use);
+        sum += x[e];
       }
+      sum += __shfl_xor(sum, 16);
       sum += __shfl_xor(sum, 32);
-      l[mt] = l[mt] * alpha + sum;
-      m[mt] = m_new;
+      l[rt] = l[rt] * alpha + sum;
+      m[rt] = m_new;
       if (!__all(alpha == 1.f)) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[mt][dt] *= alpha;
+        for (int dt = 0; dt < 8; ++dt) o[dt][rt] *= alpha;
       }
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        u32x4 w;
-        w[0] = pack_bf16x2(x[8 * s2 + 0], x[8 * s2 + 1]);
-        w[1] = pack_bf16x2(x[8 * s2 + 2], x[8 * s2 + 3]);
-        w[2] = pack_bf16x2(x[8 * s2 + 4], x[8 * s2 + 5]);
-        w[3] = pack_bf16x2(x[8 * s2 + 6], x[8 * s2 + 7]);
-        pb[mt][s2] = __builtin_bit_cast(bf16x8, w);
-      }
+      u32x4 w;
+      w[0] = pack_bf16x2(x[0], x[1]);
+      w[1] = pack_bf16x2(x[2], x[3]);
+      w[2] = pack_bf16x2(x[4], x[5]);
+      w[3] = pack_bf16x2(x[6], x[7]);
+      pb[rt] = __builtin_bit_cast(bf16x8, w);
     }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(vt[dt], pb[rt], o[dt][rt]);
+  };
 
+  // Reads the V^T operands of the tile in this wave's LDS buffer.
+  auto read_vt = [&](bf16x8 (&vt)[8]) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        uint16_t e16[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          e16[e] = *(const uint16_t*)(v_rd + (16 * s2 + (e % 4) + 8 * (e / 4)) * kLdsRow + dt * 64);
-        u32x4 w;
-        w[0] = (uint32_t)e16[0] | ((uint32_t)e16[1] << 16);
-        w[1] = (uint32_t)e16[2] | ((uint32_t)e16[3] << 16);
-        w[2] = (uint32_t)e16[4] | ((uint32_t)e16[5] << 16);
-        w[3] = (uint32_t)e16[6] | ((uint32_t)e16[7] << 16);
-        const bf16x8 va = __builtin_bit_cast(bf16x8, w);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          o[mt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[mt][s2], o[mt][dt], 0, 0, 0);
-      }
+    for (int dt = 0; dt < 8; ++dt) {
+      const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[dt]));
+      const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[dt] + 16 * 256));
+      const short e8 __attribute__((ext_vector_type(8))) = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      vt[dt] = __builtin_bit_cast(bf16x8, e8);
     }
+    lds_wave_fence();  // reads done before the buffer is refilled
   };
 
   const int first_tile = kbeg / kTile;
   const int end_tile = (kend + kTile - 1) / kTile;
+  bf16x8 kreg[2][4];
   int j = first_tile + wave;
-  if (j < end_tile) load_tile(j);
+  if (j < end_tile) {
+    const TileSrc ts = tile_src(j);
+    load_k(ts, kreg);
+    load_v(ts);
+  }
   while (j < end_tile) {
-    lds_wave_fence();  // this wave's reads of the previous tile are done before it is overwritten
-    store_tile();
-    lds_wave_fence();  // the tile is in LDS before any lane reads it
-    const int jn = j + kWaves;
-    if (jn < end_tile) load_tile(jn);  // next tile's global loads overlap this tile's math
-    compute_tile(j);
-    j = jn;
+    bf16x8 vt[8];
+    wait_vmem();
+    read_vt(vt);
+    const bool has_next = j + kWaves < end_tile;
+    TileSrc next{};
+    if (has_next) {
+      next = tile_src(j + kWaves);
+      load_v(next);  // V of the next tile refills the buffer just read
+    }
+    compute(j, kreg, vt, has_next, next);
+    j += kWaves;
   }
 
   // ---- merge the four waves in wave order ----
   __syncthreads();
-  float* ml = (float*)lds;                    // [wave][MT*32 rows][2]
-  float* ob = (float*)(lds + 4096);           // [MT*32 rows][kObRow]
-  if (hh == 0) {
+  float* ml = (float*)lds;                    // [wave][kMaxRows][2]
+  float* ob = (float*)(lds + 2048);           // [kMaxRows][kObRow]
+  if (grp == 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      ml[(wave * MT * 32 + mt * 32 + r) * 2 + 0] = m[mt];
-      ml[(wave * MT * 32 + mt * 32 + r) * 2 + 1] = l[mt];
+    for (int rt = 0; rt < RT; ++rt) {
+      ml[(wave * kMaxRows + rt * 16 + r16) * 2 + 0] = m[rt];
+      ml[(wave * kMaxRows + rt * 16 + r16) * 2 + 1] = l[rt];
     }
   }
   __syncthreads();
-  float Mrow[MT], Lrow[MT], fself[MT];
+  float Mrow[RT], Lrow[RT], fself[RT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int row = mt * 32 + r;
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = rt * 16 + r16;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[(w * MT * 32 + row) * 2]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[(w * kMaxRows + row) * 2]);
     const float M_use = M == -INFINITY ? 0.f : M;
     float L = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) L += ml[(w * MT * 32 + row) * 2 + 1] * exp2_fast(ml[(w * MT * 32 + row) * 2] - M_use);
-    Mrow[mt] = M;
-    Lrow[mt] = L;
-    fself[mt] = exp2_fast(m[mt] - M_use);
+    for (int w = 0; w < kWaves; ++w)
+      L += ml[(w * kMaxRows + row) * 2 + 1] * exp2_fast(ml[(w * kMaxRows + row) * 2] - M_use);
+    Mrow[rt] = M;
+    Lrow[rt] = L;
+    fself[rt] = exp2_fast(m[rt] - M_use);
   }
   for (int w = 0; w < kWaves; ++w) {
     if (wave == w) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        float* orow = ob + (mt * 32 + r) * kObRow;
+      for (int rt = 0; rt < RT; ++rt) {
+        float* orow = ob + (rt * 16 + r16) * kObRow + 4 * grp;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            f32x4 val;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) val[i] = o[mt][dt][4 * jj + i] * fself[mt];
-            const int d = 32 * dt + 8 * jj + 4 * hh;
-            if (w > 0) val = *(const f32x4*)(orow + d) + val;
-            if (w < kWaves - 1) {
-              *(f32x4*)(orow + d) = val;
-            } else {
-#pragma unroll
-              for (int i = 0; i < 4; ++i) o[mt][dt][4 * jj + i] = val[i];
-            }
-          }
+        for (int dt = 0; dt < 8; ++dt) {
+          f32x4 val = o[dt][rt] * fself[rt];
+          if (w > 0) val = *(const f32x4*)(orow + 16 * dt) + val;
+          if (w < kWaves - 1)
+            *(f32x4*)(orow + 16 * dt) = val;
+          else
+            o[dt][rt] = val;
         }
       }
     }
@@ -363,53 +392,44 @@ __global__ __launch_bounds__(kWaves * kWave) void attn_fwd(Params p) {
   }
   if (wave != kWaves - 1) return;
 
-  // ---- write: bf16 output (only split) or fp32 partial ----
+  // ---- write: bf16 output (only split) or fp32 partial; lane holds d = 16*dt + 4*grp + (0..3) ----
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int row = mt * 32 + r;
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = rt * 16 + r16;
     if (row >= rows) continue;
     const int i = it.p0 + row / p.g;
     const int hq = h * p.g + row % p.g;
     if (nsplit_act == 1) {
-      const float L = Lrow[mt];
-      uint16_t* op = p.out + (int64_t)(it.q_start + i) * p.out_stride + hq * kD;
+      const float L = Lrow[rt];
+      uint16_t* op = p.out + (int64_t)(it.q_start + i) * p.out_stride + hq * kD + 4 * grp;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+      for (int dt = 0; dt < 8; ++dt) {
+        float v4[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          float v4[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v4[e] = L == 0.f ? 0.f : o[mt][dt][4 * jj + e] / L;
-          uint2 w2;
-          w2.x = pack_bf16x2(v4[0], v4[1]);
-          w2.y = pack_bf16x2(v4[2], v4[3]);
-          *(uint2*)(op + 32 * dt + 8 * jj + 4 * hh) = w2;
-        }
+        for (int e = 0; e < 4; ++e) v4[e] = L == 0.f ? 0.f : o[dt][rt][e] / L;
+        uint2 w2;
+        w2.x = pack_bf16x2(v4[0], v4[1]);
+        w2.y = pack_bf16x2(v4[2], v4[3]);
+        *(uint2*)(op + 16 * dt) = w2;
       }
     } else {
       const int64_t base = (((int64_t)item * p.Hkv + h) * p.nsplit + split) * p.rows_alloc + row;
-      float* po = p.part_o + base * kD;
+      float* po = p.part_o + base * kD + 4 * grp;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          f32x4 val;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) val[e] = o[mt][dt][4 * jj + e];
-          *(f32x4*)(po + 32 * dt + 8 * jj + 4 * hh) = val;
-        }
-      }
-      if (hh == 0) {
-        p.part_ml[base * 2 + 0] = Mrow[mt];
-        p.part_ml[base * 2 + 1] = Lrow[mt];
+      for (int dt = 0; dt < 8; ++dt) *(f32x4*)(po + 16 * dt) = o[dt][rt];
+      if (grp == 0) {
+        p.part_ml[base * 2 + 0] = Mrow[rt];
+        p.part_ml[base * 2 + 1] = Lrow[rt];
       }
     }
   }
 }
 
-// Merges the fp32 split partials of items with more than one active split, in split order.
+// Merges the fp32 split partials of items with more than one active split, in split order. One wave per
+// row; each lane owns two d values; all of a row's split loads are issued before the reductions.
 template <bool kVarlen>
 __global__ __launch_bounds__(256) void attn_combine(Params p) {
+  constexpr int kMaxSplitsInRegs = 16;
   const int item = blockIdx.x;
   const int h = blockIdx.y;
   const Item it = describe<kVarlen>(p, item);
@@ -422,16 +442,41 @@ __global__ __launch_bounds__(256) void attn_combine(Params p) {
   for (int row = wave; row < rows; row += 4) {
     const int64_t base0 = (((int64_t)item * p.Hkv + h) * p.nsplit) * p.rows_alloc + row;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit_act; ++s) M = fmaxf(M, p.part_ml[(base0 + (int64_t)s * p.rows_alloc) * 2]);
-    const float M_use = M == -INFINITY ? 0.f : M;
     float L = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int s = 0; s < nsplit_act; ++s) {
-      const int64_t b = base0 + (int64_t)s * p.rows_alloc;
-      const float f = exp2_fast(p.part_ml[b * 2] - M_use);
-      L += p.part_ml[b * 2 + 1] * f;
-      const float2 ov = *(const float2*)(p.part_o + b * kD + 2 * lane);
-      o0 += ov.x * f;
-      o1 += ov.y * f;
+    for (int s0 = 0; s0 < nsplit_act; s0 += kMaxSplitsInRegs) {
+      const int ns = min(kMaxSplitsInRegs, nsplit_act - s0);
+      float ms[kMaxSplitsInRegs], ls[kMaxSplitsInRegs];
+      float2 os[kMaxSplitsInRegs];
+#pragma unroll
+      for (int s = 0; s < kMaxSplitsInRegs; ++s) {
+        if (s < ns) {
+          const int64_t b = base0 + (int64_t)(s0 + s) * p.rows_alloc;
+          const float2 mlv = *(const float2*)(p.part_ml + b * 2);
+          ms[s] = mlv.x;
+          ls[s] = mlv.y;
+          os[s] = *(const float2*)(p.part_o + b * kD + 2 * lane);
+        }
+      }
+      // running merge in split order: rescale what was accumulated when the maximum grows
+      float Mn = M;
+#pragma unroll
+      for (int s = 0; s < kMaxSplitsInRegs; ++s)
+        if (s < ns) Mn = fmaxf(Mn, ms[s]);
+      const float Mn_use = Mn == -INFINITY ? 0.f : Mn;
+      const float a = exp2_fast(M - Mn_use);
+      L *= a;
+      o0 *= a;
+      o1 *= a;
+#pragma unroll
+      for (int s = 0; s < kMaxSplitsInRegs; ++s) {
+        if (s < ns) {
+          const float f = exp2_fast(ms[s] - Mn_use);
+          L += ls[s] * f;
+          o0 += os[s].x * f;
+          o1 += os[s].y * f;
+        }
+      }
+      M = Mn;
     }
     const int i = it.p0 + row / p.g;
     const int hq = h * p.g + row % p.g;
@@ -499,23 +544,40 @@ Layout workspace_layout(int64_t items, int Hkv, int nsplit, int rows_alloc, bool
   return L;
 }
 
-// Row tiles per workgroup and positions per query group for g query heads per KV head.
-void decode_shape(int n, int g, int* MT, int* P) {
-  if (n * g <= 32) {
-    *MT = 1;
+// 16-row tiles per workgroup and positions per query group for n queries and g heads per KV head:
+// the smallest tile count that holds all n*g rows (at most 4 tiles = 64 rows; more positions make more
+// groups).
+void decode_shape(int n, int g, int* RT, int* P) {
+  const int rows = n * g;
+  if (rows <= kMaxRows) {
+    *RT = (rows + 15) / 16;
     *P = n;
   } else {
-    *MT = 2;
-    *P = min(n, 64 / g);
+    *RT = 4;
+    *P = kMaxRows / g;
   }
 }
+
+// Varlen prefill / mixed: 2 row tiles (32 rows) per group.
+constexpr int kVarlenRT = 2;
 
 int check_heads(const char* who, int Hq, int Hkv, int D) {
   if (D != kD) return fail(kUnsupported, "%s: head_dim %d not supported (only %d)", who, D, kD);
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
     return fail(kBadArgument, "%s: num_heads %d must be a positive multiple of num_kv_heads %d", who, Hq, Hkv);
-  if (Hq / Hkv > 64) return fail(kUnsupported, "%s: more than 64 query heads per KV head", who);
+  if (Hq / Hkv > 16 * kVarlenRT) return fail(kUnsupported, "%s: more than %d query heads per KV head", who, 16 * kVarlenRT);
   return kOk;
+}
+
+template <bool kVarlen, bool kPaged>
+void launch_fwd(int RT, dim3 grid, hipStream_t s, const Params& p) {
+  const dim3 block(kWaves * kWave);
+  switch (RT) {
+    case 1: hipLaunchKernelGGL((attn_fwd<1, kVarlen, kPaged>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((attn_fwd<2, kVarlen, kPaged>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((attn_fwd<3, kVarlen, kPaged>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((attn_fwd<4, kVarlen, kPaged>), grid, block, 0, s, p); break;
+  }
 }
 
 }  // namespace
@@ -528,11 +590,11 @@ extern "C" size_t sd_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q
                                                  int32_t table_width) {
   if (num_seqs <= 0 || num_query_tokens <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
   (void)head_dim;
-  int MT, P;
-  decode_shape(num_query_tokens, num_heads / num_kv_heads, &MT, &P);
+  int RT, P;
+  decode_shape(num_query_tokens, num_heads / num_kv_heads, &RT, &P);
   const int groups = (num_query_tokens + P - 1) / P;
   const int nsplit = (int)(((int64_t)table_width * block_size + kSplit - 1) / kSplit);
-  return workspace_layout((int64_t)num_seqs * groups, num_kv_heads, max(nsplit, 1), MT * 32, false).total;
+  return workspace_layout((int64_t)num_seqs * groups, num_kv_heads, max(nsplit, 1), RT * 16, false).total;
 }
 
 extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void* k_cache, const void* v_cache,
@@ -558,13 +620,13 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
       out_token_stride % 8)
     return fail(kUnsupported, "%s: q / out / caches must be 16-byte aligned with strides multiple of 8", who);
   const int g = num_heads / num_kv_heads;
-  int MT, P;
-  decode_shape(num_query_tokens, g, &MT, &P);
+  int RT, P;
+  decode_shape(num_query_tokens, g, &RT, &P);
   const int groups = (num_query_tokens + P - 1) / P;
   const int64_t items = (int64_t)num_seqs * groups;
   const int nsplit = max(1, (int)(((int64_t)table_width * block_size + kSplit - 1) / kSplit));
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
-  const Layout lay = workspace_layout(items, num_kv_heads, nsplit, MT * 32, false);
+  const Layout lay = workspace_layout(items, num_kv_heads, nsplit, RT * 16, false);
   if (!workspace || workspace_bytes < lay.total)
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
@@ -587,7 +649,7 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
   p.g = g;
   p.P = P;
   p.nsplit = nsplit;
-  p.rows_alloc = MT * 32;
+  p.rows_alloc = RT * 16;
   p.scale_log2 = scale * kLog2e;
   p.out = (uint16_t*)out;
   p.out_stride = out_token_stride;
@@ -595,11 +657,7 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
   p.part_ml = (float*)((uint8_t*)workspace + lay.part_ml);
 
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(nsplit, num_kv_heads, (unsigned)items), block(kWaves * kWave);
-  if (MT == 1)
-    hipLaunchKernelGGL((attn_fwd<1, false, true>), grid, block, 0, s, p);
-  else
-    hipLaunchKernelGGL((attn_fwd<2, false, true>), grid, block, 0, s, p);
+  launch_fwd<false, true>(RT, dim3(nsplit, num_kv_heads, (unsigned)items), s, p);
   if ((rc = check_launch(who))) return rc;
   if (nsplit > 1) {
     hipLaunchKernelGGL((attn_combine<false>), dim3((unsigned)items, num_kv_heads), dim3(256), 0, s, p);
@@ -610,15 +668,16 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
 
 namespace {
 int64_t varlen_items(int32_t num_seqs, int32_t total_q, int P) { return (int64_t)(total_q + P - 1) / P + num_seqs; }
+int varlen_positions(int g) { return max(1, 16 * kVarlenRT / g); }
 }  // namespace
 
 extern "C" size_t sd_varlen_workspace_size(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_k, int32_t num_heads,
                                            int32_t num_kv_heads, int32_t head_dim) {
   if (num_seqs <= 0 || total_q <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
   (void)head_dim;
-  const int P = max(1, 64 / (num_heads / num_kv_heads));
+  const int P = varlen_positions(num_heads / num_kv_heads);
   const int nsplit = max(1, (max_seqlen_k + kSplit - 1) / kSplit);
-  return workspace_layout(varlen_items(num_seqs, total_q, P), num_kv_heads, nsplit, 64, true).total;
+  return workspace_layout(varlen_items(num_seqs, total_q, P), num_kv_heads, nsplit, 16 * kVarlenRT, true).total;
 }
 
 extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
@@ -650,11 +709,11 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
       out_token_stride % 8 || k_token_stride % 8 || v_token_stride % 8)
     return fail(kUnsupported, "%s: q / out / k / v must be 16-byte aligned with strides multiple of 8", who);
   const int g = num_heads / num_kv_heads;
-  const int P = max(1, 64 / g);
+  const int P = varlen_positions(g);
   const int64_t items = varlen_items(num_seqs, total_q, P);
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
   const int nsplit = max(1, (max_seqlen_k + kSplit - 1) / kSplit);
-  const Layout lay = workspace_layout(items, num_kv_heads, nsplit, 64, true);
+  const Layout lay = workspace_layout(items, num_kv_heads, nsplit, 16 * kVarlenRT, true);
   if (!workspace || workspace_bytes < lay.total)
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
@@ -678,7 +737,7 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   p.g = g;
   p.P = P;
   p.nsplit = nsplit;
-  p.rows_alloc = 64;
+  p.rows_alloc = 16 * kVarlenRT;
   p.scale_log2 = scale * kLog2e;
   p.out = (uint16_t*)out;
   p.out_stride = out_token_stride;
@@ -692,11 +751,11 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(varlen_plan, dim3(1), dim3(256), 0, s, cu_seqlens_q, num_seqs, P, work, count, (int32_t)items);
   if ((rc = check_launch(who))) return rc;
-  const dim3 grid(nsplit, num_kv_heads, (unsigned)items), block(kWaves * kWave);
+  const dim3 grid(nsplit, num_kv_heads, (unsigned)items);
   if (paged)
-    hipLaunchKernelGGL((attn_fwd<2, true, true>), grid, block, 0, s, p);
+    launch_fwd<true, true>(kVarlenRT, grid, s, p);
   else
-    hipLaunchKernelGGL((attn_fwd<2, true, false>), grid, block, 0, s, p);
+    launch_fwd<true, false>(kVarlenRT, grid, s, p);
   if ((rc = check_launch(who))) return rc;
   if (nsplit > 1) {
     hipLaunchKernelGGL((attn_combine<true>), dim3((unsigned)items, num_kv_heads), dim3(256), 0, s, p);
