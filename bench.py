@@ -184,6 +184,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-extras", action="store_true", help="headline only (for profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the hot path shards by sequence or "
@@ -191,6 +193,13 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     head = bench_verify_attention(dev, args.steps, args.warmup)
     t = head["event_s"]
     achieved = head["bytes"] / t / 1e9

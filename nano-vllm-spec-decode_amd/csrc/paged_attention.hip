@@ -36,12 +36,17 @@ namespace {
 constexpr int kD = 128;                        // head_dim (Qwen3)
 constexpr int kTile = 32;                      // keys per wave step
 constexpr int kWaves = 4;                      // waves per workgroup
-constexpr int kSplit = 512;                    // keys per split
+#ifndef SD_SPLIT_KEYS
+#define SD_SPLIT_KEYS 512
+#endif
+constexpr int kSplit = SD_SPLIT_KEYS;          // keys per split
 constexpr int kVBuf = kTile * kD * 2;          // one 32-key V tile in LDS: 8 KB per wave
 constexpr int kObRow = kD + 4;                 // fp32 row stride of the cross-wave O buffer (bank padding)
 constexpr int kMaxRows = 64;                   // 16-row tiles: at most 4
 constexpr int kMergeBytes = 2048 + kMaxRows * kObRow * 4;
-constexpr int kLdsBytes = kMergeBytes > kWaves * kVBuf ? kMergeBytes : kWaves * kVBuf;
+constexpr int kLdsMain = kMergeBytes > kWaves * kVBuf ? kMergeBytes : kWaves * kVBuf;
+constexpr int kMaxSplitBlocks = kSplit / kTile + 1;  // block ids one split can touch (block_size >= 32)
+constexpr int kLdsBytes = kLdsMain + kMaxSplitBlocks * 4;
 
 #define SD_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
 #define SD_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
@@ -121,8 +126,43 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Waits for every outstanding vector-memory load of this wave (including loads into LDS).
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Max / sum over the four lanes l, l^16, l^32, l^48 (one row of a 16x16 accumulator tile), with the
+// gfx950 lane-swap instructions instead of LDS permutes. v_permlane16_swap(a, b) exchanges the odd
+// 16-lane rows of a with the even rows of b (v_permlane32_swap: upper half of a with lower half of b), so
+// with a = b = x every lane ends up holding x of itself and of its partner. Written as inline asm because
+// the compiler's builtin does not keep the second register of the pair; the s_nops cover the VALU-write /
+// permlane-read hazard on both sides.
+__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float quad_max(float x) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+  swap16(a, b);
+  x = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  a = __builtin_bit_cast(uint32_t, x);
+  b = a;
+  swap32(a, b);
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+  swap16(a, b);
+  x = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  a = __builtin_bit_cast(uint32_t, x);
+  b = a;
+  swap32(a, b);
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
+// Two fp32 -> packed bf16 (v_cvt_pk_bf16_f32, round to nearest even).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
 
 template <int RT, bool kVarlen, bool kPaged>
 __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
@@ -153,6 +193,19 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
   if (split >= nsplit_act) return;
   const int kbeg = split * kSplit;
   const int kend = min(kbeg + kSplit, it.kmax);
+
+  // The split's block ids, read once into LDS (a per-tile table load would cost a memory round trip per
+  // tile). Ids outside the table row read as -1.
+  int32_t* blk_ids = (int32_t*)(lds + kLdsMain);
+  const int first_blk = kPaged ? kbeg / p.block_size : 0;
+  if (kPaged) {
+    const int nblk = (kend - 1) / p.block_size - first_blk + 1;
+    if (tid < nblk) {
+      const int bi = first_blk + tid;
+      blk_ids[tid] = bi < p.table_width ? p.block_tables[(int64_t)it.seq * p.table_width + bi] : -1;
+    }
+    __syncthreads();
+  }
 
   // Per-row visible-key limit inside this split (bottom-right causal: query i sees Lk - Lq + i + 1 keys)
   // and the Q operand (B of S^T): lane holds row 16*rt + r16, d = 32*ks + 8*grp + e.
@@ -186,10 +239,6 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
   }
 
   uint8_t* vbuf = lds + wave * kVBuf;
-  // V fill (global_load_lds): load q puts keys 4q .. 4q+3 at bytes 1024*q + 16*lane, i.e. key
-  // t = 4q + lane/16 in slot s = lane%16, holding chunk s ^ 2*(t%8) (16-byte chunks, 8 d each).
-  const int vf_key = lane / 16;
-  const int vf_slot = lane % 16;
   // V^T reads (ds_read_b64_tr_b16): source lane reads 4 d of key tl (+16 for the second half) at
   // d = 16*dt + 4*(lane%4): chunk 2*dt + (lane%4)/2, byte 8*(lane%2) inside it.
   const int tl = 4 * grp + r16 / 4;
@@ -198,61 +247,77 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
   for (int dt = 0; dt < 8; ++dt)
     vt_off[dt] = tl * 256 + 8 * (lane % 2) + 16 * (((2 * dt + (lane % 4) / 2) ^ (2 * (tl % 8))));
 
-  // Tile addressing: K / V base of tile jt (keys past the split's end read the tile's first key instead:
-  // finite data, masked out in the softmax). An invalid block id (bad table) reads zeros, never faults.
+  // Tile addressing: K / V base of tile jt (wave-uniform byte pointers; keys past the split's end read the
+  // tile's first key instead: finite data, masked out in the softmax). An invalid block id (bad table)
+  // never faults: its K comes from block 0 and every key of the tile is masked, its V is zero-filled.
   struct TileSrc {
-    const uint16_t* kb;
-    const uint16_t* vb;
+    const uint8_t* kb;
+    const uint8_t* vb;
     int nvalid;
     bool ok;
   };
-  auto tile_src = [&](int jt) {
+  const int64_t ksb = p.k_stride * 2, vsb = p.v_stride * 2;  // bytes per key
+  auto tile_src = [&](int jt, int blk) {
     TileSrc ts;
     const int t0 = jt * kTile;
     ts.nvalid = min(kTile, kend - t0);
     ts.ok = true;
+    int64_t row0;
     if (kPaged) {
-      const int bi = t0 / p.block_size;
-      const int blk = bi < p.table_width ? p.block_tables[(int64_t)it.seq * p.table_width + bi] : -1;
       ts.ok = blk >= 0 && blk < p.num_blocks;
-      const int64_t slot0 = (int64_t)(ts.ok ? blk : 0) * p.block_size + t0 % p.block_size;
-      ts.kb = p.k + slot0 * p.k_stride + h * kD;
-      ts.vb = p.v + slot0 * p.v_stride + h * kD;
+      row0 = (int64_t)(ts.ok ? blk : 0) * p.block_size + t0 % p.block_size;
     } else {
-      const int64_t row0 = (int64_t)p.cu_k[it.seq] + t0;
-      ts.kb = p.k + row0 * p.k_stride + h * kD;
-      ts.vb = p.v + row0 * p.v_stride + h * kD;
+      row0 = (int64_t)p.cu_k[it.seq] + t0;
     }
+    ts.kb = (const uint8_t*)p.k + row0 * ksb + h * kD * 2;
+    ts.vb = (const uint8_t*)p.v + row0 * vsb + h * kD * 2;
     return ts;
   };
-  // K of a tile into registers (A of S^T): key 16*kt + r16, d = 32*ks + 8*grp + e.
+  auto tile_blk = [&](int jt) { return kPaged ? blk_ids[jt * kTile / p.block_size - first_blk] : 0; };
+  // K of a tile into registers (A of S^T): key 16*kt + r16, d = 32*ks + 8*grp + e; 32-bit lane offsets.
+  const uint32_t k_off0 = (uint32_t)(r16 * ksb) + 16 * grp;
+  const uint32_t k_off1 = k_off0 + (uint32_t)(16 * ksb);
   auto load_k = [&](const TileSrc& ts, bf16x8 (&kr)[2][4]) {
+    const uint32_t off0 = r16 < ts.nvalid ? k_off0 : 16 * grp;
+    const uint32_t off1 = 16 + r16 < ts.nvalid ? k_off1 : 16 * grp;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int tt = 16 * kt + r16;
-      const uint16_t* src = ts.kb + (int64_t)(tt < ts.nvalid ? tt : 0) * p.k_stride + 8 * grp;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kr[kt][ks] = ts.ok ? *(const bf16x8*)(src + 32 * ks) : bf16x8{};
+    for (int ks = 0; ks < 4; ++ks) {
+      kr[0][ks] = *(const bf16x8*)(ts.kb + off0 + 64 * ks);
+      kr[1][ks] = *(const bf16x8*)(ts.kb + off1 + 64 * ks);
     }
   };
-  // V of a tile into this wave's LDS buffer (global_load_lds, 1 KB per instruction).
-  auto load_v = [&](const TileSrc& ts) {
-    if (!ts.ok) {
-      for (int e = lane; e < kVBuf / 16; e += kWave) *(u32x4*)(vbuf + 16 * e) = u32x4{0, 0, 0, 0};
-      return;
-    }
+  // V of a tile: 16-byte register loads (lane loads key t = 4*qd + lane/16, chunk (lane%16) ^ 2*(t%8),
+  // so that the later LDS store of its register to slot lane%16 lands XOR-swizzled); t%8 only depends on
+  // the parity of qd. Stored to this wave's LDS buffer once the registers are free of the previous tile.
+  const int vf_key = lane / 16;
+  const int vf_slot = lane % 16;
+  const uint32_t v_c0 = 16 * (vf_slot ^ (2 * vf_key)), v_c1 = 16 * (vf_slot ^ (2 * (4 + vf_key)));
+  const uint32_t v_off0 = (uint32_t)(vf_key * vsb) + v_c0, v_off1 = (uint32_t)(vf_key * vsb) + v_c1;
+  auto load_v = [&](const TileSrc& ts, u32x4 (&vs)[8]) {
 #pragma unroll
     for (int qd = 0; qd < 8; ++qd) {
-      const int t = 4 * qd + vf_key;
-      const int chunk = vf_slot ^ (2 * (t % 8));
-      const uint16_t* src = ts.vb + (int64_t)(t < ts.nvalid ? t : 0) * p.v_stride + 8 * chunk;
-      __builtin_amdgcn_global_load_lds(SD_GPTR(src), SD_LPTR(vbuf + 1024 * qd), 16, 0, 0);
+      const bool valid = 4 * qd + vf_key < ts.nvalid;
+      const uint32_t off = (qd % 2) ? (valid ? v_off1 : v_c1) : (valid ? v_off0 : v_c0);
+      vs[qd] = *(const u32x4*)(ts.vb + (valid ? (int64_t)(4 * qd) * vsb : 0) + off);
     }
+  };
+  auto store_v = [&](const u32x4 (&vs)[8], bool ok) {
+#pragma unroll
+    for (int qd = 0; qd < 8; ++qd) *(u32x4*)(vbuf + 1024 * qd + 16 * lane) = ok ? vs[qd] : u32x4{0, 0, 0, 0};
   };
 
   // One tile: S^T from the K registers, then (registers free) the next tile's K loads, then the online
   // softmax and O^T += V^T P^T.
-  auto compute = [&](int jt, bf16x8 (&kr)[2][4], const bf16x8 (&vt)[8], bool has_next, const TileSrc& next) {
+  // V^T operand of d-tile dt (16 d x 32 keys) from this wave's LDS buffer: two transposed reads.
+  auto read_vt = [&](int dt) {
+    const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[dt]));
+    const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[dt] + 16 * 256));
+    const short e8 __attribute__((ext_vector_type(8))) = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(bf16x8, e8);
+  };
+
+  auto compute = [&](int jt, bool tile_ok, bf16x8 (&kr)[2][4], bool has_next, const TileSrc& next) {
     const int t0 = jt * kTile;
     f32x4 s[2][RT];
 #pragma unroll
@@ -266,18 +331,18 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
       }
     if (has_next) load_k(next, kr);
     bf16x8 pb[RT];
+    const int tok0 = t0 + 4 * grp;  // keys of this lane: tok0 + (e%4) + 16*(e/4)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
+      const int lim_e = (tile_ok ? lim[rt] : t0) - tok0;
       float x[8];
       float mx = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int tok = t0 + 16 * (e / 4) + 4 * grp + (e % 4);
-        x[e] = tok < lim[rt] ? s[e / 4][rt][e % 4] * p.scale_log2 : -INFINITY;
+        x[e] = (e % 4) + 16 * (e / 4) < lim_e ? s[e / 4][rt][e % 4] * p.scale_log2 : -INFINITY;
         mx = fmaxf(mx, x[e]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = quad_max(mx);
       const float m_new = fmaxf(m[rt], mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = exp2_fast(m[rt] - m_use);
@@ -287,8 +352,7 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
         x[e] = exp2_fast(x[e] - m_use);
         sum += x[e];
       }
-      sum += __shfl_xor(sum, 16);
-      sum += __shfl_xor(sum, 32);
+      sum = quad_sum(sum);
       l[rt] = l[rt] * alpha + sum;
       m[rt] = m_new;
       if (!__all(alpha == 1.f)) {
@@ -296,51 +360,45 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
         for (int dt = 0; dt < 8; ++dt) o[dt][rt] *= alpha;
       }
       u32x4 w;
-      w[0] = pack_bf16x2(x[0], x[1]);
-      w[1] = pack_bf16x2(x[2], x[3]);
-      w[2] = pack_bf16x2(x[4], x[5]);
-      w[3] = pack_bf16x2(x[6], x[7]);
+      w[0] = cvt_bf16x2(x[0], x[1]);
+      w[1] = cvt_bf16x2(x[2], x[3]);
+      w[2] = cvt_bf16x2(x[4], x[5]);
+      w[3] = cvt_bf16x2(x[6], x[7]);
       pb[rt] = __builtin_bit_cast(bf16x8, w);
     }
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(vt[dt], pb[rt], o[dt][rt]);
-  };
-
-  // Reads the V^T operands of the tile in this wave's LDS buffer.
-  auto read_vt = [&](bf16x8 (&vt)[8]) {
-#pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[dt]));
-      const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[dt] + 16 * 256));
-      const short e8 __attribute__((ext_vector_type(8))) = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-      vt[dt] = __builtin_bit_cast(bf16x8, e8);
+      const bf16x8 vt = read_vt(dt);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(vt, pb[rt], o[dt][rt]);
     }
-    lds_wave_fence();  // reads done before the buffer is refilled
   };
 
   const int first_tile = kbeg / kTile;
   const int end_tile = (kend + kTile - 1) / kTile;
   bf16x8 kreg[2][4];
+  u32x4 vstage[8];
   int j = first_tile + wave;
+  bool cur_ok = true;
   if (j < end_tile) {
-    const TileSrc ts = tile_src(j);
+    const TileSrc ts = tile_src(j, __builtin_amdgcn_readfirstlane(tile_blk(j)));
     load_k(ts, kreg);
-    load_v(ts);
+    load_v(ts, vstage);
+    cur_ok = ts.ok;
   }
   while (j < end_tile) {
-    bf16x8 vt[8];
-    wait_vmem();
-    read_vt(vt);
     const bool has_next = j + kWaves < end_tile;
+    const int blk_next = has_next ? tile_blk(j + kWaves) : 0;
+    lds_wave_fence();          // previous tile's V^T reads (and the block id read) are complete
+    store_v(vstage, cur_ok);   // waits for this tile's V registers
     TileSrc next{};
     if (has_next) {
-      next = tile_src(j + kWaves);
-      load_v(next);  // V of the next tile refills the buffer just read
+      next = tile_src(j + kWaves, __builtin_amdgcn_readfirstlane(blk_next));
+      load_v(next, vstage);    // next tile's V in flight during this tile's math
     }
-    compute(j, kreg, vt, has_next, next);
+    lds_wave_fence();          // the tile is in LDS before any lane reads it
+    compute(j, cur_ok, kreg, has_next, next);
+    cur_ok = next.ok;
     j += kWaves;
   }
 
@@ -408,8 +466,8 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
 #pragma unroll
         for (int e = 0; e < 4; ++e) v4[e] = L == 0.f ? 0.f : o[dt][rt][e] / L;
         uint2 w2;
-        w2.x = pack_bf16x2(v4[0], v4[1]);
-        w2.y = pack_bf16x2(v4[2], v4[3]);
+        w2.x = cvt_bf16x2(v4[0], v4[1]);
+        w2.y = cvt_bf16x2(v4[2], v4[3]);
         *(uint2*)(op + 16 * dt) = w2;
       }
     } else {
@@ -483,7 +541,7 @@ __global__ __launch_bounds__(256) void attn_combine(Params p) {
     uint16_t* op = p.out + (int64_t)(it.q_start + i) * p.out_stride + hq * kD;
     const float r0 = L == 0.f ? 0.f : o0 / L;
     const float r1 = L == 0.f ? 0.f : o1 / L;
-    *(uint32_t*)(op + 2 * lane) = pack_bf16x2(r0, r1);
+    *(uint32_t*)(op + 2 * lane) = cvt_bf16x2(r0, r1);
   }
 }
 
