@@ -2,29 +2,33 @@
 // nanovllm/layers/attention.py:71-78) and for varlen prefill / mixed prefill+decode (replaces
 // flash_attn_varlen_func, attention.py:64-70). One kernel family serves both.
 //
-// Work decomposition. A work item is (sequence, query group, KV head, key split):
+// Work decomposition. A work item is (sequence, query group, KV head):
 //   * query group: P consecutive query positions of one sequence; with g = Hq/Hkv heads sharing the KV
 //     head, the group holds P*g "rows" (row r = position r/g, head r%g) — GQA head-group sharing: the
 //     KV stream is read once for all g query heads.
-//   * key split: a fixed 512-key range [512*s, 512*(s+1)). Split boundaries never depend on batch size,
-//     query count or context length, and partial results are merged in a fixed order, so a row's output
-//     is bitwise independent of the batch it runs in (decode vs verify vs mixed).
-// A 256-thread workgroup (4 waves) handles one item; wave w streams the 32-key tiles w, w+4, w+8, ... of
-// the split with bf16 MFMA 16x16x32 (rows in 16-row tiles, RT of them):
+//   * the item's keys are cut into 32-key tiles; tile t belongs to residue t % 8. One wave streams the
+//     tiles of one residue in increasing order with an online softmax, giving a partial (max, sum, O) per
+//     row; the 8 residue partials are merged in residue order 0..7 with a fixed fma chain. This reduction
+//     tree depends on nothing but the key positions, so a row's output is bitwise independent of the
+//     batch size, of the number of query rows per sequence and of whether the step is a decode, a verify
+//     or a mixed step.
+// How residues map to hardware is chosen per launch from the amount of work, without changing the
+// arithmetic: with many items one 8-wave workgroup owns an item's 8 residues and merges them in LDS
+// (no workspace, no second kernel); with few items each workgroup owns 1, 2 or 4 residues, writes their
+// partials to the workspace, and attn_combine runs the same merge.
+//
+// Per tile a wave computes, with bf16 MFMA 16x16x32 (rows in 16-row tiles, RT of them):
 //   S^T[16 keys x 16 rows] = K[16 x 128] . Q^T      A = K straight from HBM into registers (16 B per
 //                                                    lane, 64 contiguous bytes per key row per load),
-//                                                    B = Q in registers for the whole split
+//                                                    B = Q in registers for the whole item
 //   O^T[16 d x 16 rows]   += V^T[16 x 32] . P^T      A = V^T read transposed from LDS with
 //                                                    ds_read_b64_tr_b16, B = P straight from S^T's
 //                                                    accumulators (the key order inside the 32-key
 //                                                    k-step is permuted identically for P and V^T)
-// V reaches LDS by global_load_lds_dwordx4 (no register staging): each lane fetches the 16-byte chunk
-// that lands, XOR-swizzled, in its own LDS slot, so the transposed reads are bank-conflict free. The next
-// tile's K (registers) and V (LDS) loads are issued right after the current tile's V^T is read, so
-// 16 KB per wave stay in flight while the MFMAs and the online softmax run; at <= 256 VGPRs two
-// workgroups share a CU. The four waves' (max, sum, O) are merged in LDS in wave order; a split that is
-// its item's only one writes bf16 output directly, otherwise fp32 partials go to the workspace and
-// attn_combine merges the splits in order.
+// V is loaded 16 B per lane into registers, each lane fetching the chunk that its LDS store places,
+// XOR-swizzled, so that the transposed reads are bank-conflict free. The next tile's V loads are issued
+// as soon as the current V is in LDS and its K loads as soon as S^T is computed, so 16 KB per wave are
+// in flight while the MFMAs and the softmax run; at <= 256 VGPRs two waves share a SIMD.
 #include <math.h>
 
 #include "sd_common.h"
@@ -35,21 +39,22 @@ namespace {
 
 constexpr int kD = 128;                        // head_dim (Qwen3)
 constexpr int kTile = 32;                      // keys per wave step
-constexpr int kWaves = 4;                      // waves per workgroup
-#ifndef SD_SPLIT_KEYS
-#define SD_SPLIT_KEYS 512
-#endif
-constexpr int kSplit = SD_SPLIT_KEYS;          // keys per split
+constexpr int kResidues = 8;                   // tile t belongs to residue t % 8
 constexpr int kVBuf = kTile * kD * 2;          // one 32-key V tile in LDS: 8 KB per wave
-constexpr int kObRow = kD + 4;                 // fp32 row stride of the cross-wave O buffer (bank padding)
+constexpr int kObRow = kD + 4;                 // fp32 row stride of the merge buffer (bank padding)
 constexpr int kMaxRows = 64;                   // 16-row tiles: at most 4
-constexpr int kMergeBytes = 2048 + kMaxRows * kObRow * 4;
-constexpr int kLdsMain = kMergeBytes > kWaves * kVBuf ? kMergeBytes : kWaves * kVBuf;
-constexpr int kMaxSplitBlocks = kSplit / kTile + 1;  // block ids one split can touch (block_size >= 32)
-constexpr int kLdsBytes = kLdsMain + kMaxSplitBlocks * 4;
+constexpr int kMaxBlocks = 1024;               // block-table entries staged in LDS per item
+constexpr int kMlBytes = kResidues * kMaxRows * 2 * 4;
+constexpr int kObBytes = kMaxRows * kObRow * 4;
 
-#define SD_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
-#define SD_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
+// LDS of a workgroup with `waves` waves: one V buffer per wave (reused as the merge buffer when the
+// workgroup merges all eight residues), the merge's (max, sum) table, and the item's block ids.
+constexpr int stage_bytes(int waves) {
+  return waves == kResidues ? (waves * kVBuf > kObBytes ? waves * kVBuf : kObBytes) : waves * kVBuf;
+}
+constexpr int ml_bytes(int waves) { return waves == kResidues ? kMlBytes : 0; }
+constexpr int lds_bytes(int waves) { return stage_bytes(waves) + ml_bytes(waves) + kMaxBlocks * 4; }
+
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 struct Params {
@@ -72,13 +77,12 @@ struct Params {
   int32_t total_q;              // tokens in q
   int64_t total_k;              // varlen without block table: rows in k / v
   int32_t Hq, Hkv, g, P;
-  int32_t nsplit;               // grid.x: splits allocated per item
-  int32_t rows_alloc;           // rows per (item, head, split) partial
+  int32_t rows_alloc;           // rows per (item, head, residue) partial
   float scale_log2;             // softmax scale * log2(e)
   uint16_t* out;
   int64_t out_stride;
-  float* part_o;                // [item][Hkv][nsplit][rows_alloc][kD]
-  float* part_ml;               // [item][Hkv][nsplit][rows_alloc][2] = (max, sum)
+  float* part_o;                // [item][Hkv][kResidues][rows_alloc][kD]
+  float* part_ml;               // [item][Hkv][kResidues][rows_alloc][2] = (max, sum)
 };
 
 struct Item {
@@ -111,7 +115,6 @@ __device__ __forceinline__ Item describe(const Params& p, int item) {
   }
   if (p.block_tables && (int64_t)it.Lk > (int64_t)p.table_width * p.block_size)
     it.Lk = p.table_width * p.block_size;  // never index past the table row
-  if ((int64_t)it.Lk > (int64_t)p.nsplit * kSplit) it.Lk = p.nsplit * kSplit;  // never past the allocated splits
   it.p0 = grp * p.P;
   it.np = min(p.P, it.Lq - it.p0);
   if (it.np <= 0) return it;
@@ -164,51 +167,44 @@ __device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
-template <int RT, bool kVarlen, bool kPaged>
-__global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+// The residue merge used by both the in-workgroup path and attn_combine: M = max_r m_r; then, residue by
+// residue in order 0..7, L = fma(l_r, f_r, L) and O = fma(O_r, f_r, O) from 0 with f_r = 2^(m_r - M);
+// out = O / L (0 when L == 0). Explicit fmas keep the rounding identical in both places.
+__device__ __forceinline__ float merge_scale(float m_r, float M) {
+  return exp2_fast(m_r - (M == -INFINITY ? 0.f : M));
+}
 
-  const int split = blockIdx.x;
+template <int RT, bool kVarlen, bool kPaged, int kWaves>
+__global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes(kWaves)];
+  constexpr bool kMergeHere = kWaves == kResidues;
+  constexpr int kStageBytes = stage_bytes(kWaves);
+
   const int h = blockIdx.y;
   const int item = blockIdx.z;
   const Item it = describe<kVarlen>(p, item);
   if (!it.valid) return;
-  const int nsplit_act = (it.kmax + kSplit - 1) / kSplit;
   const int rows = it.np * p.g;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int residue = blockIdx.x * kWaves + wave;
   const int lane = tid % kWave;
   const int r16 = lane % 16;  // row (S^T / O^T column) or key (K operand row) owned by this lane
   const int grp = lane / 16;  // 16-lane group: which 8 k-elements / 4 accumulator rows
+  const int kmax = it.kmax;
+  const int end_tile = (kmax + kTile - 1) / kTile;
 
-  if (it.kmax <= 0) {  // no row sees any key (e.g. context_len 0 padding): zeros, written once
-    if (split != 0) return;
-    for (int e = tid; e < rows * (kD / 8); e += kWaves * kWave) {
-      const int row = e / (kD / 8), c = e % (kD / 8);
-      const int i = it.p0 + row / p.g, hq = h * p.g + row % p.g;
-      *(u32x4*)(p.out + (int64_t)(it.q_start + i) * p.out_stride + hq * kD + c * 8) = u32x4{0, 0, 0, 0};
-    }
-    return;
-  }
-  if (split >= nsplit_act) return;
-  const int kbeg = split * kSplit;
-  const int kend = min(kbeg + kSplit, it.kmax);
-
-  // The split's block ids, read once into LDS (a per-tile table load would cost a memory round trip per
-  // tile). Ids outside the table row read as -1.
-  int32_t* blk_ids = (int32_t*)(lds + kLdsMain);
-  const int first_blk = kPaged ? kbeg / p.block_size : 0;
+  // The item's block ids, read once into LDS; ids outside the table row read as -1.
+  int32_t* blk_ids = (int32_t*)(lds + kStageBytes + ml_bytes(kWaves));
   if (kPaged) {
-    const int nblk = (kend - 1) / p.block_size - first_blk + 1;
-    if (tid < nblk) {
-      const int bi = first_blk + tid;
-      blk_ids[tid] = bi < p.table_width ? p.block_tables[(int64_t)it.seq * p.table_width + bi] : -1;
-    }
+    const int nblk = min((kmax + p.block_size - 1) / p.block_size, kMaxBlocks);
+    for (int b = tid; b < nblk; b += kWaves * kWave)
+      blk_ids[b] = b < p.table_width ? p.block_tables[(int64_t)it.seq * p.table_width + b] : -1;
     __syncthreads();
   }
 
-  // Per-row visible-key limit inside this split (bottom-right causal: query i sees Lk - Lq + i + 1 keys)
-  // and the Q operand (B of S^T): lane holds row 16*rt + r16, d = 32*ks + 8*grp + e.
+  // Per-row visible-key limit (bottom-right causal: query i sees Lk - Lq + i + 1 keys) and the Q operand
+  // (B of S^T): lane holds row 16*rt + r16, d = 32*ks + 8*grp + e.
   int lim[RT];
   bf16x8 qv[RT][4];
 #pragma unroll
@@ -217,12 +213,12 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
     if (row < rows) {
       const int i = it.p0 + row / p.g;
       const int hq = h * p.g + row % p.g;
-      lim[rt] = min(max(it.Lk - it.Lq + i + 1, 0), kend);
+      lim[rt] = min(max(it.Lk - it.Lq + i + 1, 0), kmax);
       const uint16_t* qp = p.q + (int64_t)(it.q_start + i) * p.q_stride + hq * kD + 8 * grp;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) qv[rt][ks] = *(const bf16x8*)(qp + 32 * ks);
     } else {
-      lim[rt] = kend;  // padding row: Q = 0 keeps its scores finite; never written
+      lim[rt] = kmax;  // padding row: Q = 0 keeps its scores finite; never written
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) qv[rt][ks] = bf16x8{};
     }
@@ -247,9 +243,9 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
   for (int dt = 0; dt < 8; ++dt)
     vt_off[dt] = tl * 256 + 8 * (lane % 2) + 16 * (((2 * dt + (lane % 4) / 2) ^ (2 * (tl % 8))));
 
-  // Tile addressing: K / V base of tile jt (wave-uniform byte pointers; keys past the split's end read the
+  // Tile addressing: K / V base of tile jt (wave-uniform byte pointers; keys past the item's end read the
   // tile's first key instead: finite data, masked out in the softmax). An invalid block id (bad table)
-  // never faults: its K comes from block 0 and every key of the tile is masked, its V is zero-filled.
+  // never faults: its K and V come from block 0 and every key of the tile is masked, its V zero-filled.
   struct TileSrc {
     const uint8_t* kb;
     const uint8_t* vb;
@@ -260,7 +256,7 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
   auto tile_src = [&](int jt, int blk) {
     TileSrc ts;
     const int t0 = jt * kTile;
-    ts.nvalid = min(kTile, kend - t0);
+    ts.nvalid = min(kTile, kmax - t0);
     ts.ok = true;
     int64_t row0;
     if (kPaged) {
@@ -273,7 +269,10 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
     ts.vb = (const uint8_t*)p.v + row0 * vsb + h * kD * 2;
     return ts;
   };
-  auto tile_blk = [&](int jt) { return kPaged ? blk_ids[jt * kTile / p.block_size - first_blk] : 0; };
+  auto tile_blk = [&](int jt) {
+    const int bi = jt * kTile / p.block_size;
+    return kPaged ? (bi < kMaxBlocks ? blk_ids[bi] : -1) : 0;
+  };
   // K of a tile into registers (A of S^T): key 16*kt + r16, d = 32*ks + 8*grp + e; 32-bit lane offsets.
   const uint32_t k_off0 = (uint32_t)(r16 * ksb) + 16 * grp;
   const uint32_t k_off1 = k_off0 + (uint32_t)(16 * ksb);
@@ -288,7 +287,7 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
   };
   // V of a tile: 16-byte register loads (lane loads key t = 4*qd + lane/16, chunk (lane%16) ^ 2*(t%8),
   // so that the later LDS store of its register to slot lane%16 lands XOR-swizzled); t%8 only depends on
-  // the parity of qd. Stored to this wave's LDS buffer once the registers are free of the previous tile.
+  // the parity of qd. Stored to this wave's LDS buffer once the previous tile's V^T has been read.
   const int vf_key = lane / 16;
   const int vf_slot = lane % 16;
   const uint32_t v_c0 = 16 * (vf_slot ^ (2 * vf_key)), v_c1 = 16 * (vf_slot ^ (2 * (4 + vf_key)));
@@ -305,9 +304,6 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
 #pragma unroll
     for (int qd = 0; qd < 8; ++qd) *(u32x4*)(vbuf + 1024 * qd + 16 * lane) = ok ? vs[qd] : u32x4{0, 0, 0, 0};
   };
-
-  // One tile: S^T from the K registers, then (registers free) the next tile's K loads, then the online
-  // softmax and O^T += V^T P^T.
   // V^T operand of d-tile dt (16 d x 32 keys) from this wave's LDS buffer: two transposed reads.
   auto read_vt = [&](int dt) {
     const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[dt]));
@@ -317,6 +313,8 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
     return __builtin_bit_cast(bf16x8, e8);
   };
 
+  // One tile: S^T from the K registers, then (registers free) the next tile's K loads, then the online
+  // softmax and O^T += V^T P^T.
   auto compute = [&](int jt, bool tile_ok, bf16x8 (&kr)[2][4], bool has_next, const TileSrc& next) {
     const int t0 = jt * kTile;
     f32x4 s[2][RT];
@@ -374,11 +372,9 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
     }
   };
 
-  const int first_tile = kbeg / kTile;
-  const int end_tile = (kend + kTile - 1) / kTile;
   bf16x8 kreg[2][4];
   u32x4 vstage[8];
-  int j = first_tile + wave;
+  int j = residue;
   bool cur_ok = true;
   if (j < end_tile) {
     const TileSrc ts = tile_src(j, __builtin_amdgcn_readfirstlane(tile_blk(j)));
@@ -387,77 +383,93 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
     cur_ok = ts.ok;
   }
   while (j < end_tile) {
-    const bool has_next = j + kWaves < end_tile;
-    const int blk_next = has_next ? tile_blk(j + kWaves) : 0;
+    const bool has_next = j + kResidues < end_tile;
+    const int blk_next = has_next ? tile_blk(j + kResidues) : 0;
     lds_wave_fence();          // previous tile's V^T reads (and the block id read) are complete
     store_v(vstage, cur_ok);   // waits for this tile's V registers
     TileSrc next{};
     if (has_next) {
-      next = tile_src(j + kWaves, __builtin_amdgcn_readfirstlane(blk_next));
+      next = tile_src(j + kResidues, __builtin_amdgcn_readfirstlane(blk_next));
       load_v(next, vstage);    // next tile's V in flight during this tile's math
     }
     lds_wave_fence();          // the tile is in LDS before any lane reads it
     compute(j, cur_ok, kreg, has_next, next);
     cur_ok = next.ok;
-    j += kWaves;
+    j += kResidues;
   }
 
-  // ---- merge the four waves in wave order ----
-  __syncthreads();
-  float* ml = (float*)lds;                    // [wave][kMaxRows][2]
-  float* ob = (float*)(lds + 2048);           // [kMaxRows][kObRow]
-  if (grp == 0) {
+  if constexpr (!kMergeHere) {
+    // ---- write this residue's partial; attn_combine merges the eight ----
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      ml[(wave * kMaxRows + rt * 16 + r16) * 2 + 0] = m[rt];
-      ml[(wave * kMaxRows + rt * 16 + r16) * 2 + 1] = l[rt];
-    }
-  }
-  __syncthreads();
-  float Mrow[RT], Lrow[RT], fself[RT];
+      const int row = rt * 16 + r16;
+      if (row >= rows) continue;
+      const int64_t base = (((int64_t)item * p.Hkv + h) * kResidues + residue) * p.rows_alloc + row;
+      float* po = p.part_o + base * kD + 4 * grp;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int row = rt * 16 + r16;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[(w * kMaxRows + row) * 2]);
-    const float M_use = M == -INFINITY ? 0.f : M;
-    float L = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-      L += ml[(w * kMaxRows + row) * 2 + 1] * exp2_fast(ml[(w * kMaxRows + row) * 2] - M_use);
-    Mrow[rt] = M;
-    Lrow[rt] = L;
-    fself[rt] = exp2_fast(m[rt] - M_use);
-  }
-  for (int w = 0; w < kWaves; ++w) {
-    if (wave == w) {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        float* orow = ob + (rt * 16 + r16) * kObRow + 4 * grp;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          f32x4 val = o[dt][rt] * fself[rt];
-          if (w > 0) val = *(const f32x4*)(orow + 16 * dt) + val;
-          if (w < kWaves - 1)
-            *(f32x4*)(orow + 16 * dt) = val;
-          else
-            o[dt][rt] = val;
-        }
+      for (int dt = 0; dt < 8; ++dt) *(f32x4*)(po + 16 * dt) = o[dt][rt];
+      if (grp == 0) {
+        p.part_ml[base * 2 + 0] = m[rt];
+        p.part_ml[base * 2 + 1] = l[rt];
       }
     }
-    if (w < kWaves - 1) __syncthreads();
-  }
-  if (wave != kWaves - 1) return;
-
-  // ---- write: bf16 output (only split) or fp32 partial; lane holds d = 16*dt + 4*grp + (0..3) ----
+    return;
+  } else {
+    // ---- merge the eight residues in order in LDS (same arithmetic as attn_combine) ----
+    __syncthreads();
+    float* ml = (float*)(lds + kStageBytes);  // [residue][kMaxRows][2]
+    float* ob = (float*)lds;                  // [kMaxRows][kObRow], over the V buffers
+    if (grp == 0) {
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int row = rt * 16 + r16;
-    if (row >= rows) continue;
-    const int i = it.p0 + row / p.g;
-    const int hq = h * p.g + row % p.g;
-    if (nsplit_act == 1) {
+      for (int rt = 0; rt < RT; ++rt) {
+        ml[(wave * kMaxRows + rt * 16 + r16) * 2 + 0] = m[rt];
+        ml[(wave * kMaxRows + rt * 16 + r16) * 2 + 1] = l[rt];
+      }
+    }
+    __syncthreads();
+    float Lrow[RT], fself[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int row = rt * 16 + r16;
+      float M = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < kResidues; ++r) M = fmaxf(M, ml[(r * kMaxRows + row) * 2]);
+      float L = 0.f;
+#pragma unroll
+      for (int r = 0; r < kResidues; ++r)
+        L = __builtin_fmaf(ml[(r * kMaxRows + row) * 2 + 1], merge_scale(ml[(r * kMaxRows + row) * 2], M), L);
+      Lrow[rt] = L;
+      fself[rt] = merge_scale(m[rt], M);
+    }
+    for (int r = 0; r < kResidues; ++r) {
+      if (wave == r) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          float* orow = ob + (rt * 16 + r16) * kObRow + 4 * grp;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) {
+            const f32x4 prev = r > 0 ? *(const f32x4*)(orow + 16 * dt) : f32x4{};
+            f32x4 val;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) val[e] = __builtin_fmaf(o[dt][rt][e], fself[rt], prev[e]);
+            if (r < kResidues - 1)
+              *(f32x4*)(orow + 16 * dt) = val;
+            else
+              o[dt][rt] = val;
+          }
+        }
+      }
+      if (r < kResidues - 1) __syncthreads();
+    }
+    if (wave != kResidues - 1) return;
+
+    // ---- bf16 output; lane holds d = 16*dt + 4*grp + (0..3) ----
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int row = rt * 16 + r16;
+      if (row >= rows) continue;
+      const int i = it.p0 + row / p.g;
+      const int hq = h * p.g + row % p.g;
       const float L = Lrow[rt];
       uint16_t* op = p.out + (int64_t)(it.q_start + i) * p.out_stride + hq * kD + 4 * grp;
 #pragma unroll
@@ -470,71 +482,43 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
         w2.y = cvt_bf16x2(v4[2], v4[3]);
         *(uint2*)(op + 16 * dt) = w2;
       }
-    } else {
-      const int64_t base = (((int64_t)item * p.Hkv + h) * p.nsplit + split) * p.rows_alloc + row;
-      float* po = p.part_o + base * kD + 4 * grp;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) *(f32x4*)(po + 16 * dt) = o[dt][rt];
-      if (grp == 0) {
-        p.part_ml[base * 2 + 0] = Mrow[rt];
-        p.part_ml[base * 2 + 1] = Lrow[rt];
-      }
     }
   }
 }
 
-// Merges the fp32 split partials of items with more than one active split, in split order. One wave per
-// row; each lane owns two d values; all of a row's split loads are issued before the reductions.
+// Merges the eight residue partials of every row, in residue order, with the same fma chain as the
+// in-workgroup merge. One wave per row; each lane owns two d values.
 template <bool kVarlen>
 __global__ __launch_bounds__(256) void attn_combine(Params p) {
-  constexpr int kMaxSplitsInRegs = 16;
   const int item = blockIdx.x;
   const int h = blockIdx.y;
   const Item it = describe<kVarlen>(p, item);
   if (!it.valid) return;
-  const int nsplit_act = (it.kmax + kSplit - 1) / kSplit;
-  if (nsplit_act <= 1) return;
   const int rows = it.np * p.g;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   for (int row = wave; row < rows; row += 4) {
-    const int64_t base0 = (((int64_t)item * p.Hkv + h) * p.nsplit) * p.rows_alloc + row;
+    const int64_t base0 = (((int64_t)item * p.Hkv + h) * kResidues) * p.rows_alloc + row;
+    float ms[kResidues], ls[kResidues];
+    float2 os[kResidues];
+#pragma unroll
+    for (int r = 0; r < kResidues; ++r) {
+      const int64_t b = base0 + (int64_t)r * p.rows_alloc;
+      const float2 mlv = *(const float2*)(p.part_ml + b * 2);
+      ms[r] = mlv.x;
+      ls[r] = mlv.y;
+      os[r] = *(const float2*)(p.part_o + b * kD + 2 * lane);
+    }
     float M = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < kResidues; ++r) M = fmaxf(M, ms[r]);
     float L = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int s0 = 0; s0 < nsplit_act; s0 += kMaxSplitsInRegs) {
-      const int ns = min(kMaxSplitsInRegs, nsplit_act - s0);
-      float ms[kMaxSplitsInRegs], ls[kMaxSplitsInRegs];
-      float2 os[kMaxSplitsInRegs];
 #pragma unroll
-      for (int s = 0; s < kMaxSplitsInRegs; ++s) {
-        if (s < ns) {
-          const int64_t b = base0 + (int64_t)(s0 + s) * p.rows_alloc;
-          const float2 mlv = *(const float2*)(p.part_ml + b * 2);
-          ms[s] = mlv.x;
-          ls[s] = mlv.y;
-          os[s] = *(const float2*)(p.part_o + b * kD + 2 * lane);
-        }
-      }
-      // running merge in split order: rescale what was accumulated when the maximum grows
-      float Mn = M;
-#pragma unroll
-      for (int s = 0; s < kMaxSplitsInRegs; ++s)
-        if (s < ns) Mn = fmaxf(Mn, ms[s]);
-      const float Mn_use = Mn == -INFINITY ? 0.f : Mn;
-      const float a = exp2_fast(M - Mn_use);
-      L *= a;
-      o0 *= a;
-      o1 *= a;
-#pragma unroll
-      for (int s = 0; s < kMaxSplitsInRegs; ++s) {
-        if (s < ns) {
-          const float f = exp2_fast(ms[s] - Mn_use);
-          L += ls[s] * f;
-          o0 += os[s].x * f;
-          o1 += os[s].y * f;
-        }
-      }
-      M = Mn;
+    for (int r = 0; r < kResidues; ++r) {
+      const float f = merge_scale(ms[r], M);
+      L = __builtin_fmaf(ls[r], f, L);
+      o0 = __builtin_fmaf(os[r].x, f, o0);
+      o1 = __builtin_fmaf(os[r].y, f, o1);
     }
     const int i = it.p0 + row / p.g;
     const int hq = h * p.g + row % p.g;
@@ -591,9 +575,11 @@ struct Layout {
   size_t part_o, part_ml, work, count, total;
 };
 
-Layout workspace_layout(int64_t items, int Hkv, int nsplit, int rows_alloc, bool varlen) {
+// Workspace: residue partials only when the merge runs in attn_combine (few items), plus the varlen
+// work list.
+Layout workspace_layout(int64_t items, int Hkv, int rows_alloc, bool partials, bool varlen) {
   Layout L;
-  const int64_t cells = items * Hkv * nsplit * rows_alloc;
+  const int64_t cells = partials ? items * Hkv * kResidues * rows_alloc : 0;
   L.part_o = 0;
   L.part_ml = align256(L.part_o + (size_t)cells * kD * sizeof(float));
   L.work = align256(L.part_ml + (size_t)cells * 2 * sizeof(float));
@@ -602,8 +588,8 @@ Layout workspace_layout(int64_t items, int Hkv, int nsplit, int rows_alloc, bool
   return L;
 }
 
-// 16-row tiles per workgroup and positions per query group for n queries and g heads per KV head:
-// the smallest tile count that holds all n*g rows (at most 4 tiles = 64 rows; more positions make more
+// 16-row tiles per item and positions per query group for n queries and g heads per KV head: the
+// smallest tile count that holds all n*g rows (at most 4 tiles = 64 rows; more positions make more
 // groups).
 void decode_shape(int n, int g, int* RT, int* P) {
   const int rows = n * g;
@@ -619,22 +605,55 @@ void decode_shape(int n, int g, int* RT, int* P) {
 // Varlen prefill / mixed: 2 row tiles (32 rows) per group.
 constexpr int kVarlenRT = 2;
 
+// Waves per workgroup: all eight residues in one workgroup (merge in LDS) when there are enough
+// (item, head) pairs to fill the GPU and the per-wave state allows two waves per SIMD; otherwise fewer
+// residues per workgroup and more workgroups, with the merge in attn_combine.
+int residue_waves(int64_t items, int Hkv, int RT) {
+  const int64_t pairs = items * Hkv;
+  if (RT <= 2 && pairs >= 256) return 8;
+  if (pairs >= 128) return 4;
+  if (pairs >= 32) return 2;
+  return 1;
+}
+
 int check_heads(const char* who, int Hq, int Hkv, int D) {
   if (D != kD) return fail(kUnsupported, "%s: head_dim %d not supported (only %d)", who, D, kD);
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
     return fail(kBadArgument, "%s: num_heads %d must be a positive multiple of num_kv_heads %d", who, Hq, Hkv);
-  if (Hq / Hkv > 16 * kVarlenRT) return fail(kUnsupported, "%s: more than %d query heads per KV head", who, 16 * kVarlenRT);
+  if (Hq / Hkv > 16 * kVarlenRT)
+    return fail(kUnsupported, "%s: more than %d query heads per KV head", who, 16 * kVarlenRT);
   return kOk;
 }
 
+template <int RT, bool kVarlen, bool kPaged>
+void launch_rt(int waves, dim3 items_grid, hipStream_t s, const Params& p) {
+  const dim3 grid(kResidues / waves, items_grid.y, items_grid.z);
+  switch (waves) {
+    case 8: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 8>), grid, dim3(8 * kWave), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 4>), grid, dim3(4 * kWave), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 2>), grid, dim3(2 * kWave), 0, s, p); break;
+    default: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 1>), grid, dim3(kWave), 0, s, p); break;
+  }
+}
+
+// Row tiles 3 and 4 need more than 256 registers per wave, so they never run eight waves per workgroup.
+template <int RT, bool kVarlen, bool kPaged>
+void launch_rt_small(int waves, dim3 items_grid, hipStream_t s, const Params& p) {
+  const dim3 grid(kResidues / waves, items_grid.y, items_grid.z);
+  switch (waves) {
+    case 4: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 4>), grid, dim3(4 * kWave), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 2>), grid, dim3(2 * kWave), 0, s, p); break;
+    default: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 1>), grid, dim3(kWave), 0, s, p); break;
+  }
+}
+
 template <bool kVarlen, bool kPaged>
-void launch_fwd(int RT, dim3 grid, hipStream_t s, const Params& p) {
-  const dim3 block(kWaves * kWave);
+void launch_fwd(int RT, int waves, dim3 grid, hipStream_t s, const Params& p) {
   switch (RT) {
-    case 1: hipLaunchKernelGGL((attn_fwd<1, kVarlen, kPaged>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((attn_fwd<2, kVarlen, kPaged>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((attn_fwd<3, kVarlen, kPaged>), grid, block, 0, s, p); break;
-    default: hipLaunchKernelGGL((attn_fwd<4, kVarlen, kPaged>), grid, block, 0, s, p); break;
+    case 1: launch_rt<1, kVarlen, kPaged>(waves, grid, s, p); break;
+    case 2: launch_rt<2, kVarlen, kPaged>(waves, grid, s, p); break;
+    case 3: launch_rt_small<3, kVarlen, kPaged>(waves, grid, s, p); break;
+    default: launch_rt_small<4, kVarlen, kPaged>(waves, grid, s, p); break;
   }
 }
 
@@ -648,11 +667,13 @@ extern "C" size_t sd_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q
                                                  int32_t table_width) {
   if (num_seqs <= 0 || num_query_tokens <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
   (void)head_dim;
+  (void)block_size;
+  (void)table_width;
   int RT, P;
   decode_shape(num_query_tokens, num_heads / num_kv_heads, &RT, &P);
-  const int groups = (num_query_tokens + P - 1) / P;
-  const int nsplit = (int)(((int64_t)table_width * block_size + kSplit - 1) / kSplit);
-  return workspace_layout((int64_t)num_seqs * groups, num_kv_heads, max(nsplit, 1), RT * 16, false).total;
+  const int64_t items = (int64_t)num_seqs * ((num_query_tokens + P - 1) / P);
+  const bool partials = residue_waves(items, num_kv_heads, RT) < kResidues;
+  return workspace_layout(items, num_kv_heads, RT * 16, partials, false).total;
 }
 
 extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void* k_cache, const void* v_cache,
@@ -669,6 +690,8 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
                 num_query_tokens, table_width, (long long)num_blocks);
   if (block_size <= 0 || block_size % kTile)
     return fail(kUnsupported, "%s: block_size %d must be a positive multiple of %d", who, block_size, kTile);
+  if (table_width > kMaxBlocks)
+    return fail(kUnsupported, "%s: table width %d exceeds %d blocks", who, table_width, kMaxBlocks);
   if (num_seqs == 0) return kOk;
   if (!q || !k_cache || !v_cache || !context_lens || !block_tables || !out)
     return fail(kBadArgument, "%s: null pointer", who);
@@ -682,10 +705,11 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
   decode_shape(num_query_tokens, g, &RT, &P);
   const int groups = (num_query_tokens + P - 1) / P;
   const int64_t items = (int64_t)num_seqs * groups;
-  const int nsplit = max(1, (int)(((int64_t)table_width * block_size + kSplit - 1) / kSplit));
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
-  const Layout lay = workspace_layout(items, num_kv_heads, nsplit, RT * 16, false);
-  if (!workspace || workspace_bytes < lay.total)
+  const int waves = residue_waves(items, num_kv_heads, RT);
+  const bool partials = waves < kResidues;
+  const Layout lay = workspace_layout(items, num_kv_heads, RT * 16, partials, false);
+  if (partials && (!workspace || workspace_bytes < lay.total))
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
   Params p{};
@@ -706,18 +730,17 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
   p.Hkv = num_kv_heads;
   p.g = g;
   p.P = P;
-  p.nsplit = nsplit;
   p.rows_alloc = RT * 16;
   p.scale_log2 = scale * kLog2e;
   p.out = (uint16_t*)out;
   p.out_stride = out_token_stride;
-  p.part_o = (float*)((uint8_t*)workspace + lay.part_o);
-  p.part_ml = (float*)((uint8_t*)workspace + lay.part_ml);
+  p.part_o = partials ? (float*)((uint8_t*)workspace + lay.part_o) : nullptr;
+  p.part_ml = partials ? (float*)((uint8_t*)workspace + lay.part_ml) : nullptr;
 
   hipStream_t s = (hipStream_t)stream;
-  launch_fwd<false, true>(RT, dim3(nsplit, num_kv_heads, (unsigned)items), s, p);
+  launch_fwd<false, true>(RT, waves, dim3(1, num_kv_heads, (unsigned)items), s, p);
   if ((rc = check_launch(who))) return rc;
-  if (nsplit > 1) {
+  if (partials) {
     hipLaunchKernelGGL((attn_combine<false>), dim3((unsigned)items, num_kv_heads), dim3(256), 0, s, p);
     if ((rc = check_launch(who))) return rc;
   }
@@ -733,9 +756,11 @@ extern "C" size_t sd_varlen_workspace_size(int32_t num_seqs, int32_t total_q, in
                                            int32_t num_kv_heads, int32_t head_dim) {
   if (num_seqs <= 0 || total_q <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
   (void)head_dim;
+  (void)max_seqlen_k;
   const int P = varlen_positions(num_heads / num_kv_heads);
-  const int nsplit = max(1, (max_seqlen_k + kSplit - 1) / kSplit);
-  return workspace_layout(varlen_items(num_seqs, total_q, P), num_kv_heads, nsplit, 16 * kVarlenRT, true).total;
+  const int64_t items = varlen_items(num_seqs, total_q, P);
+  const bool partials = residue_waves(items, num_kv_heads, kVarlenRT) < kResidues;
+  return workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true).total;
 }
 
 extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
@@ -758,6 +783,8 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
       return fail(kBadArgument, "%s: paged mode needs a block table, blocks and a block_size multiple of %d", who, kTile);
     if (k_token_stride != (int64_t)num_kv_heads * head_dim || v_token_stride != k_token_stride)
       return fail(kBadArgument, "%s: paged caches must have token stride num_kv_heads*head_dim", who);
+    if (table_width > kMaxBlocks)
+      return fail(kUnsupported, "%s: table width %d exceeds %d blocks", who, table_width, kMaxBlocks);
   } else if (k_token_stride < (int64_t)num_kv_heads * head_dim || v_token_stride < (int64_t)num_kv_heads * head_dim) {
     return fail(kBadArgument, "%s: k / v token stride smaller than num_kv_heads*head_dim", who);
   }
@@ -770,8 +797,9 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   const int P = varlen_positions(g);
   const int64_t items = varlen_items(num_seqs, total_q, P);
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
-  const int nsplit = max(1, (max_seqlen_k + kSplit - 1) / kSplit);
-  const Layout lay = workspace_layout(items, num_kv_heads, nsplit, 16 * kVarlenRT, true);
+  const int waves = residue_waves(items, num_kv_heads, kVarlenRT);
+  const bool partials = waves < kResidues;
+  const Layout lay = workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true);
   if (!workspace || workspace_bytes < lay.total)
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
@@ -794,13 +822,12 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   p.Hkv = num_kv_heads;
   p.g = g;
   p.P = P;
-  p.nsplit = nsplit;
   p.rows_alloc = 16 * kVarlenRT;
   p.scale_log2 = scale * kLog2e;
   p.out = (uint16_t*)out;
   p.out_stride = out_token_stride;
-  p.part_o = (float*)((uint8_t*)workspace + lay.part_o);
-  p.part_ml = (float*)((uint8_t*)workspace + lay.part_ml);
+  p.part_o = partials ? (float*)((uint8_t*)workspace + lay.part_o) : nullptr;
+  p.part_ml = partials ? (float*)((uint8_t*)workspace + lay.part_ml) : nullptr;
   int32_t* work = (int32_t*)((uint8_t*)workspace + lay.work);
   int32_t* count = (int32_t*)((uint8_t*)workspace + lay.count);
   p.work = work;
@@ -809,13 +836,13 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(varlen_plan, dim3(1), dim3(256), 0, s, cu_seqlens_q, num_seqs, P, work, count, (int32_t)items);
   if ((rc = check_launch(who))) return rc;
-  const dim3 grid(nsplit, num_kv_heads, (unsigned)items);
+  const dim3 grid(1, num_kv_heads, (unsigned)items);
   if (paged)
-    launch_fwd<true, true>(kVarlenRT, grid, s, p);
+    launch_rt<kVarlenRT, true, true>(waves, grid, s, p);
   else
-    launch_fwd<true, false>(kVarlenRT, grid, s, p);
+    launch_rt<kVarlenRT, true, false>(waves, grid, s, p);
   if ((rc = check_launch(who))) return rc;
-  if (nsplit > 1) {
+  if (partials) {
     hipLaunchKernelGGL((attn_combine<true>), dim3((unsigned)items, num_kv_heads), dim3(256), 0, s, p);
     if ((rc = check_launch(who))) return rc;
   }
