@@ -45,10 +45,12 @@ constexpr int kObRow = kD + 4;                 // fp32 row stride of the merge b
 constexpr int kMaxRows = 64;                   // 16-row tiles: at most 4
 constexpr int kMaxBlocks = 1024;               // block-table entries staged in LDS per item
 constexpr int kMlBytes = kResidues * kMaxRows * 2 * 4;
-constexpr int kObBytes = kMaxRows * kObRow * 4;
+constexpr int kMergeRows = 32;                 // rows merged in LDS (row tiles 1-2)
+constexpr int kObBytes = kResidues * kMergeRows * kObRow * 4;
 
-// LDS of a workgroup with `waves` waves: one V buffer per wave (reused as the merge buffer when the
-// workgroup merges all eight residues), the merge's (max, sum) table, and the item's block ids.
+// LDS of a workgroup with `waves` waves: one V buffer per wave (when the workgroup merges all eight
+// residues the same bytes then hold every residue's O), the merge's (max, sum) table, and the item's
+// block ids.
 constexpr int stage_bytes(int waves) {
   return waves == kResidues ? (waves * kVBuf > kObBytes ? waves * kVBuf : kObBytes) : waves * kVBuf;
 }
@@ -182,24 +184,48 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
 
   const int h = blockIdx.y;
   const int item = blockIdx.z;
-  const Item it = describe<kVarlen>(p, item);
-  if (!it.valid) return;
-  const int rows = it.np * p.g;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int residue = blockIdx.x * kWaves + wave;
   const int lane = tid % kWave;
   const int r16 = lane % 16;  // row (S^T / O^T column) or key (K operand row) owned by this lane
   const int grp = lane / 16;  // 16-lane group: which 8 k-elements / 4 accumulator rows
+  int32_t* blk_ids = (int32_t*)(lds + kStageBytes + ml_bytes(kWaves));
+
+  // Decode items know their sequence without a memory read: start the block-table row loads (the whole
+  // row, ids are range-checked before use) before the context length arrives, so the prologue costs one
+  // memory round trip instead of two.
+  constexpr int kBlkPerThread = (kMaxBlocks + kWaves * kWave - 1) / (kWaves * kWave);
+  int32_t blk_pre[kBlkPerThread];
+  const int nblk_row = min(p.table_width, kMaxBlocks);
+  if (kPaged && !kVarlen) {
+    const int seq = item / p.groups_per_seq;
+#pragma unroll
+    for (int i = 0; i < kBlkPerThread; ++i) {
+      const int b = tid + i * kWaves * kWave;
+      blk_pre[i] = b < nblk_row ? p.block_tables[(int64_t)seq * p.table_width + b] : -1;
+    }
+  }
+  const Item it = describe<kVarlen>(p, item);
+  if (!it.valid) return;
+  const int rows = it.np * p.g;
   const int kmax = it.kmax;
   const int end_tile = (kmax + kTile - 1) / kTile;
 
-  // The item's block ids, read once into LDS; ids outside the table row read as -1.
-  int32_t* blk_ids = (int32_t*)(lds + kStageBytes + ml_bytes(kWaves));
+  // The item's block ids in LDS.
   if (kPaged) {
-    const int nblk = min((kmax + p.block_size - 1) / p.block_size, kMaxBlocks);
-    for (int b = tid; b < nblk; b += kWaves * kWave)
-      blk_ids[b] = b < p.table_width ? p.block_tables[(int64_t)it.seq * p.table_width + b] : -1;
+    if (kVarlen) {
+#pragma unroll
+      for (int i = 0; i < kBlkPerThread; ++i) {
+        const int b = tid + i * kWaves * kWave;
+        blk_pre[i] = b < nblk_row ? p.block_tables[(int64_t)it.seq * p.table_width + b] : -1;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kBlkPerThread; ++i) {
+      const int b = tid + i * kWaves * kWave;
+      if (b < nblk_row) blk_ids[b] = blk_pre[i];
+    }
     __syncthreads();
   }
 
@@ -271,7 +297,7 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
   };
   auto tile_blk = [&](int jt) {
     const int bi = jt * kTile / p.block_size;
-    return kPaged ? (bi < kMaxBlocks ? blk_ids[bi] : -1) : 0;
+    return kPaged ? (bi < nblk_row ? blk_ids[bi] : -1) : 0;
   };
   // K of a tile into registers (A of S^T): key 16*kt + r16, d = 32*ks + 8*grp + e; 32-bit lane offsets.
   const uint32_t k_off0 = (uint32_t)(r16 * ksb) + 16 * grp;
@@ -415,10 +441,12 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
     }
     return;
   } else {
-    // ---- merge the eight residues in order in LDS (same arithmetic as attn_combine) ----
-    __syncthreads();
+    // ---- merge the eight residues in order: every wave parks its O in LDS, then each thread finishes
+    // eight consecutive d of one row with the same fma chain as attn_combine ----
+    static_assert(RT * 16 <= kMergeRows, "in-workgroup merge holds at most 32 rows");
+    __syncthreads();  // all V^T reads done: the V buffers become the O store
     float* ml = (float*)(lds + kStageBytes);  // [residue][kMaxRows][2]
-    float* ob = (float*)lds;                  // [kMaxRows][kObRow], over the V buffers
+    float* ob = (float*)lds;                  // [residue][kMergeRows][kObRow]
     if (grp == 0) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
@@ -426,62 +454,41 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
         ml[(wave * kMaxRows + rt * 16 + r16) * 2 + 1] = l[rt];
       }
     }
-    __syncthreads();
-    float Lrow[RT], fself[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const int row = rt * 16 + r16;
+      float* orow = ob + (wave * kMergeRows + rt * 16 + r16) * kObRow + 4 * grp;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) *(f32x4*)(orow + 16 * dt) = o[dt][rt];
+    }
+    __syncthreads();
+    constexpr int kThreads = kWaves * kWave;
+    for (int e0 = tid * 8; e0 < RT * 16 * kD; e0 += kThreads * 8) {
+      const int row = e0 / kD, d0 = e0 % kD;
+      if (row >= rows) continue;
       float M = -INFINITY;
 #pragma unroll
       for (int r = 0; r < kResidues; ++r) M = fmaxf(M, ml[(r * kMaxRows + row) * 2]);
       float L = 0.f;
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < kResidues; ++r)
-        L = __builtin_fmaf(ml[(r * kMaxRows + row) * 2 + 1], merge_scale(ml[(r * kMaxRows + row) * 2], M), L);
-      Lrow[rt] = L;
-      fself[rt] = merge_scale(m[rt], M);
-    }
-    for (int r = 0; r < kResidues; ++r) {
-      if (wave == r) {
+      for (int r = 0; r < kResidues; ++r) {
+        const float f = merge_scale(ml[(r * kMaxRows + row) * 2], M);
+        L = __builtin_fmaf(ml[(r * kMaxRows + row) * 2 + 1], f, L);
+        const float* src = ob + (r * kMergeRows + row) * kObRow + d0;
+        const f32x4 a = *(const f32x4*)src, b = *(const f32x4*)(src + 4);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          float* orow = ob + (rt * 16 + r16) * kObRow + 4 * grp;
-#pragma unroll
-          for (int dt = 0; dt < 8; ++dt) {
-            const f32x4 prev = r > 0 ? *(const f32x4*)(orow + 16 * dt) : f32x4{};
-            f32x4 val;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) val[e] = __builtin_fmaf(o[dt][rt][e], fself[rt], prev[e]);
-            if (r < kResidues - 1)
-              *(f32x4*)(orow + 16 * dt) = val;
-            else
-              o[dt][rt] = val;
-          }
+        for (int e = 0; e < 4; ++e) {
+          acc[e] = __builtin_fmaf(a[e], f, acc[e]);
+          acc[4 + e] = __builtin_fmaf(b[e], f, acc[4 + e]);
         }
       }
-      if (r < kResidues - 1) __syncthreads();
-    }
-    if (wave != kResidues - 1) return;
-
-    // ---- bf16 output; lane holds d = 16*dt + 4*grp + (0..3) ----
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const int row = rt * 16 + r16;
-      if (row >= rows) continue;
       const int i = it.p0 + row / p.g;
       const int hq = h * p.g + row % p.g;
-      const float L = Lrow[rt];
-      uint16_t* op = p.out + (int64_t)(it.q_start + i) * p.out_stride + hq * kD + 4 * grp;
+      u32x4 w;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        float v4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v4[e] = L == 0.f ? 0.f : o[dt][rt][e] / L;
-        uint2 w2;
-        w2.x = cvt_bf16x2(v4[0], v4[1]);
-        w2.y = cvt_bf16x2(v4[2], v4[3]);
-        *(uint2*)(op + 16 * dt) = w2;
-      }
+      for (int e = 0; e < 4; ++e)
+        w[e] = cvt_bf16x2(L == 0.f ? 0.f : acc[2 * e] / L, L == 0.f ? 0.f : acc[2 * e + 1] / L);
+      *(u32x4*)(p.out + (int64_t)(it.q_start + i) * p.out_stride + hq * kD + d0) = w;
     }
   }
 }
