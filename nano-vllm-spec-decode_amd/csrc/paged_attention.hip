@@ -398,30 +398,36 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
     }
   };
 
+  // The loop body issues its loads unconditionally and the last tile is peeled: with a conditional load
+  // in the body the compiler's wait counts must cover the path without it and would wait for the next
+  // tile's V before this tile's S^T.
   bf16x8 kreg[2][4];
   u32x4 vstage[8];
   int j = residue;
   bool cur_ok = true;
   if (j < end_tile) {
     const TileSrc ts = tile_src(j, __builtin_amdgcn_readfirstlane(tile_blk(j)));
-    load_k(ts, kreg);
     load_v(ts, vstage);
+    load_k(ts, kreg);
     cur_ok = ts.ok;
   }
-  while (j < end_tile) {
-    const bool has_next = j + kResidues < end_tile;
-    const int blk_next = has_next ? tile_blk(j + kResidues) : 0;
+  while (j + kResidues < end_tile) {
+    const int blk_next = tile_blk(j + kResidues);
     lds_wave_fence();          // previous tile's V^T reads (and the block id read) are complete
     store_v(vstage, cur_ok);   // waits for this tile's V registers
-    TileSrc next{};
-    if (has_next) {
-      next = tile_src(j + kResidues, __builtin_amdgcn_readfirstlane(blk_next));
-      load_v(next, vstage);    // next tile's V in flight during this tile's math
-    }
+    const TileSrc next = tile_src(j + kResidues, __builtin_amdgcn_readfirstlane(blk_next));
+    load_v(next, vstage);      // next tile's V in flight during this tile's math
+    __builtin_amdgcn_sched_barrier(0);  // keep those loads ahead of the S^T MFMAs
     lds_wave_fence();          // the tile is in LDS before any lane reads it
-    compute(j, cur_ok, kreg, has_next, next);
+    compute(j, cur_ok, kreg, true, next);
     cur_ok = next.ok;
     j += kResidues;
+  }
+  if (j < end_tile) {
+    lds_wave_fence();
+    store_v(vstage, cur_ok);
+    lds_wave_fence();
+    compute(j, cur_ok, kreg, false, TileSrc{});
   }
 
   if constexpr (!kMergeHere) {
