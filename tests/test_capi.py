@@ -39,8 +39,13 @@ def test_abi_version(lib):
 
 
 def test_workspace_sizes(lib):
-    # headline verify: 64 sequences x 1 group x 8 kv heads x 17 splits x 32 rows x (128 + 2) fp32
-    assert lib.sd_paged_decode_workspace_size(64, 5, 32, 8, 128, 256, 33) >= 64 * 8 * 17 * 32 * 130 * 4
+    # 64 sequences x 8 kv heads = 512 (item, head) pairs fill the GPU with 8-wave workgroups that merge
+    # their residues in LDS: no workspace.
+    assert lib.sd_paged_decode_workspace_size(64, 5, 32, 8, 128, 256, 33) == 0
+    # 16 sequences: residue partials [16 items][8 heads][8 residues][32 rows] x (128 + 2) fp32
+    assert lib.sd_paged_decode_workspace_size(16, 5, 32, 8, 128, 256, 33) >= 16 * 8 * 8 * 32 * 130 * 4
+    # 9 queries x 4 heads = 36 rows -> 3 row tiles, which never merge in LDS
+    assert lib.sd_paged_decode_workspace_size(64, 9, 32, 8, 128, 256, 33) >= 64 * 8 * 8 * 48 * 130 * 4
     assert lib.sd_paged_decode_workspace_size(0, 5, 32, 8, 128, 256, 33) == 0
     assert lib.sd_varlen_workspace_size(51, 2048, 4096, 32, 8, 128) > 0
     assert lib.sd_verify_workspace_size(64, 4, 151936, 1) >= (64 * 5 + 64 * 4) * 38 * 16
