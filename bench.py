@@ -4,12 +4,14 @@ Headline (value): speculative-verify paged attention at Qwen3-8B shapes — 32 q
 128, bf16 KV cache in 256-token blocks, B = 64 sequences, k = 4 guesses (5 causal queries each), context
 4096 — as algorithmic HBM TB/s: the bytes one call must move (every KV byte of every sequence, the queries,
 the outputs, the block-table entries and context lengths) divided by the measured time. One step = one call
-(one layer). Inputs are resident in HBM before the timed region.
+(one layer). Inputs are resident in HBM before the timed region. `roofline.traffic` is the HBM bytes per
+launch that rocprofv3's FETCH_SIZE + WRITE_SIZE counters measured for this launch (committed summary under
+profiles/), null if that summary is absent.
 
 Also reported (same JSON line): the KV-cache scatter (2048 rows, 10% padding slots), the rejection sampler
 (S 64, K 4, V 151936, T 0 and T 1 with draft logits) and a 2048-token mixed prefill+decode attention step
-over 36 layers (tok/s), plus a CPU baseline: the oracle (PyTorch CPU restatement) on a bounded sample of
-the headline workload.
+over 36 layers (tok/s), plus a CPU baseline: the oracle (PyTorch CPU restatement) timed on the headline
+workload for about 10 s on 16 host threads.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10]
 """
@@ -39,21 +41,26 @@ def decode_bytes(ctx, n):
 
 
 def timed(fn, steps, warmup):
-    """Runs fn warmup times, then `steps` times between two synchronizations; returns (seconds per step,
-    per-call event durations in seconds) measured with events on the current stream."""
+    """Runs fn warmup times, then `steps` back-to-back times between two synchronizations (the wall clock of
+    that region gives seconds per step), then `steps` more times with an event pair around each call on the
+    current stream (the stream every kernel of this package launches on) for the per-launch durations.
+    Returns (seconds per step, [per-call event seconds])."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    t0 = time.perf_counter()
     for i in range(steps):
         starts[i].record()
         fn()
         ends[i].record()
     torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
     ev = [s.elapsed_time(e) / 1e3 for s, e in zip(starts, ends)]
     return wall, ev
 
@@ -151,31 +158,40 @@ def bench_mixed_attention(dev, steps, warmup, layers=36):
                 prefill_flops_per_layer=flops, decode_bytes_per_layer=dec_bytes)
 
 
-def cpu_baseline(inputs, sample_seqs=2):
-    """The oracle (fp32 PyTorch CPU restatement of the reference semantics) on `sample_seqs` of the headline
-    sequences, all host threads; returns GB/s of algorithmic bytes."""
+def cpu_baseline(inputs, min_seconds=10.0, max_reps=8):
+    """The oracle (fp32 PyTorch CPU restatement of the reference semantics) on the headline workload: all
+    64 sequences, repeated until at least `min_seconds` of CPU work have been timed (at most `max_reps`
+    runs, after one untimed 2-sequence warm-up), on 16 host threads; returns GB/s of algorithmic bytes."""
     import torch
     from oracle import attention as oatt
     q, kc, vc, lens, tables = inputs
     torch.set_num_threads(min(16, os.cpu_count() or 1))   # the GPU box grants 16 host cores per GPU
-    qs = q[:sample_seqs].cpu()
-    ls = lens[:sample_seqs].cpu()
-    ts = tables[:sample_seqs].cpu()
-    used = sorted({int(b) for b in ts.flatten().tolist() if b >= 0})
-    remap = {b: i for i, b in enumerate(used)}
-    kcs = kc[used].cpu()
-    vcs = vc[used].cpu()
-    ts = ts.clone().apply_(lambda b: remap.get(b, -1))
-    times = []
-    for _ in range(3):
+    qs, ls, ts = q.cpu(), lens.cpu(), tables.cpu()
+    kcs, vcs = kc.cpu(), vc.cpu()
+    oatt.paged_decode_attention(qs[:2], kcs, vcs, ls[:2], ts[:2], D ** -0.5)
+    reps, total = 0, 0.0
+    while reps < max_reps and (total < min_seconds or reps < 2):
         t0 = time.perf_counter()
         oatt.paged_decode_attention(qs, kcs, vcs, ls, ts, D ** -0.5)
-        times.append(time.perf_counter() - t0)
-    t = min(times)
+        total += time.perf_counter() - t0
+        reps += 1
+    t = total / reps
     nbytes = decode_bytes(ls.tolist(), q.size(1))
-    return dict(value=nbytes / t / 1e9, unit="GB/s", cores=torch.get_num_threads(), kind="port",
-                sample=f"{sample_seqs} of the 64 sequences (ctx 4096, k=4), oracle paged_decode_attention, "
-                       f"min of 3 runs ({t * 1e3:.0f} ms)")
+    return dict(value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"the full headline call (64 sequences, ctx 4096, k=4) through the oracle's "
+                       f"paged_decode_attention, {reps} runs, {total:.1f} s total, {t * 1e3:.0f} ms per call")
+
+
+def pmc_traffic(path=os.path.join(ROOT, "profiles", "attn_fwd_verify_b64_k4_ctx4096.pmc.txt")):
+    """HBM bytes per headline launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each
+    counter scaled by what it reads for a plain 1 GiB device copy); None when the summary is absent."""
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -184,6 +200,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-extras", action="store_true", help="headline only (for profiling)")
+    ap.add_argument("--no-cpu", action="store_true", help="leave out the CPU baseline (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -221,8 +238,8 @@ def main():
                                "B=64, k=4 (5 causal queries), ctx 4096, block 256, table width 33",
                    "batch": 64, "k": 4, "context": 4096, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "attn_fwd + attn_combine (one sd_paged_decode call)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
+                     "kernel": "attn_fwd<RT=2, 8 waves> (one sd_paged_decode call: one launch, residues merged in LDS)",
                      "bytes_per_launch": head["bytes"], "us_per_launch": round(t * 1e6, 2)},
     }
     if not args.skip_extras:
@@ -230,6 +247,7 @@ def main():
         result["verify_sampler"] = bench_sampler(dev, max(10, args.steps // 2), args.warmup)
         mixed = bench_mixed_attention(dev, max(5, args.steps // 10), 2)
         result["mixed_step_attention"] = mixed
+    if not args.skip_extras and not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(head["inputs"])
     print(json.dumps(result), flush=True)
 

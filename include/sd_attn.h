@@ -58,8 +58,12 @@ int sd_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
  * q holds num_seqs * num_query_tokens tokens (sequence-major). context_lens[b] counts the cached keys
  * including the sequence's num_query_tokens new ones; query i sees keys 0 .. context_lens[b]-n+i
  * (bottom-right causal). context_lens[b] == 0 (padding sequence) writes zeros.
- * Keys are processed in fixed 512-token splits combined in a fixed order, so a row's result does not
- * depend on num_seqs, num_query_tokens or the other rows (bitwise).
+ * Keys are cut into 32-key tiles; tile t belongs to residue t % 8, each residue is reduced with an online
+ * softmax in increasing tile order and the eight residue partials are merged in residue order with a fixed
+ * fma chain. That reduction depends only on key positions, so a row's result does not depend on num_seqs,
+ * num_query_tokens or the other rows (bitwise), and equals the row's result from sd_varlen_attention.
+ * The workspace (residue partials) is needed only when the call has too few (sequence, KV head) pairs to
+ * merge inside one workgroup; sd_paged_decode_workspace_size returns 0 otherwise.
  */
 size_t sd_paged_decode_workspace_size(int32_t num_seqs, int32_t num_query_tokens, int32_t num_heads,
                                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
