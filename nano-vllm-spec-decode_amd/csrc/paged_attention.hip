@@ -31,6 +31,10 @@
 // in flight while the MFMAs and the softmax run; at <= 256 VGPRs two waves share a SIMD.
 #include <math.h>
 
+#include <algorithm>
+#include <climits>
+
+#include "prefill_attention.h"
 #include "sd_common.h"
 #include "../../include/sd_attn.h"
 
@@ -125,24 +129,11 @@ __device__ __forceinline__ Item describe(const Params& p, int item) {
   return it;
 }
 
-__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Max / sum over the four lanes l, l^16, l^32, l^48 (one row of a 16x16 accumulator tile), with the
-// gfx950 lane-swap instructions instead of LDS permutes. v_permlane16_swap(a, b) exchanges the odd
-// 16-lane rows of a with the even rows of b (v_permlane32_swap: upper half of a with lower half of b), so
-// with a = b = x every lane ends up holding x of itself and of its partner. Written as inline asm because
-// the compiler's builtin does not keep the second register of the pair; the s_nops cover the VALU-write /
-// permlane-read hazard on both sides.
-__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-}
+// Max / sum over the four lanes l, l^16, l^32, l^48 (one row of a 16x16 accumulator tile).
 __device__ __forceinline__ float quad_max(float x) {
   uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
   swap16(a, b);
@@ -160,13 +151,6 @@ __device__ __forceinline__ float quad_sum(float x) {
   b = a;
   swap32(a, b);
   return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
-}
-
-// Two fp32 -> packed bf16 (v_cvt_pk_bf16_f32, round to nearest even).
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
 // The residue merge used by both the in-workgroup path and attn_combine: M = max_r m_r; then, residue by
@@ -542,42 +526,77 @@ __global__ __launch_bounds__(256) void attn_combine(Params p) {
   }
 }
 
-// Varlen work list: every sequence contributes ceil(Lq / P) (sequence, group) items, in order.
-__global__ __launch_bounds__(256) void varlen_plan(const int32_t* __restrict__ cu_q, int32_t num_seqs, int32_t P,
-                                                   int32_t* __restrict__ work, int32_t* __restrict__ count,
-                                                   int32_t max_items) {
-  __shared__ int32_t scan[256];
-  __shared__ int32_t carry;
-  const int tid = threadIdx.x;
-  if (tid == 0) carry = 0;
+// Varlen work lists. A sequence with 1..kResidueMaxQ queries contributes ceil(Lq / P_res) (sequence, group)
+// items of the residue kernel; a longer one contributes ceil(Lq / P_pre) (sequence, q-block) items of the
+// prefill kernel, its last q-block (the one that sees the most keys) first. One 1024-thread workgroup: each
+// pass scans 1024 sequences (wave prefix sums, then the wave totals).
+constexpr int kPlanThreads = 1024;
+__device__ __forceinline__ int wave_inclusive_sum(int x, int lane) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __restrict__ cu_q, int32_t num_seqs,
+                                                            int32_t P_res, int32_t P_pre,
+                                                            int32_t* __restrict__ work_res, int32_t* __restrict__ count_res,
+                                                            int32_t max_res, int32_t* __restrict__ work_pre,
+                                                            int32_t* __restrict__ count_pre, int32_t max_pre) {
+  constexpr int kPlanWaves = kPlanThreads / kWave;
+  __shared__ int32_t wsum[2][kPlanWaves];
+  __shared__ int32_t carry[2];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  if (tid < 2) carry[tid] = 0;
   __syncthreads();
-  for (int base = 0; base < num_seqs; base += 256) {
+  for (int base = 0; base < num_seqs; base += kPlanThreads) {
     const int s = base + tid;
-    int ng = 0;
-    if (s < num_seqs) {
-      const int Lq = cu_q[s + 1] - cu_q[s];
-      ng = Lq > 0 ? (Lq + P - 1) / P : 0;
+    int Lq = 0;
+    if (s < num_seqs) Lq = max(cu_q[s + 1] - cu_q[s], 0);
+    const int nr = Lq > 0 && Lq <= kResidueMaxQ ? (Lq + P_res - 1) / P_res : 0;
+    const int nq = Lq > kResidueMaxQ ? (Lq + P_pre - 1) / P_pre : 0;
+    const int ir = wave_inclusive_sum(nr, lane);
+    const int iq = wave_inclusive_sum(nq, lane);
+    if (lane == kWave - 1) {
+      wsum[0][wave] = ir;
+      wsum[1][wave] = iq;
     }
-    scan[tid] = ng;
     __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-      const int add = tid >= off ? scan[tid - off] : 0;
-      __syncthreads();
-      scan[tid] += add;
-      __syncthreads();
+    int offr = carry[0], offq = carry[1], totr = 0, totq = 0;
+    for (int w = 0; w < kPlanWaves; ++w) {
+      if (w < wave) {
+        offr += wsum[0][w];
+        offq += wsum[1][w];
+      }
+      totr += wsum[0][w];
+      totq += wsum[1][w];
     }
-    const int start = carry + scan[tid] - ng;
-    for (int gi = 0; gi < ng; ++gi) {
-      if (start + gi < max_items) {
-        work[2 * (start + gi)] = s;
-        work[2 * (start + gi) + 1] = gi;
+    const int start_r = offr + ir - nr, start_q = offq + iq - nq;
+    for (int i = 0; i < nr; ++i) {
+      if (start_r + i < max_res) {
+        work_res[2 * (start_r + i)] = s;
+        work_res[2 * (start_r + i) + 1] = i;
+      }
+    }
+    for (int i = 0; i < nq; ++i) {
+      if (start_q + i < max_pre) {
+        work_pre[2 * (start_q + i)] = s;
+        work_pre[2 * (start_q + i) + 1] = nq - 1 - i;
       }
     }
     __syncthreads();
-    if (tid == 255) carry += scan[255];
+    if (tid == 0) {
+      carry[0] += totr;
+      carry[1] += totq;
+    }
     __syncthreads();
   }
-  if (tid == 0) *count = min(carry, max_items);
+  if (tid == 0) {
+    *count_res = min(carry[0], max_res);
+    *count_pre = min(carry[1], max_pre);
+  }
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -585,19 +604,21 @@ constexpr float kLog2e = 1.4426950408889634f;
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Layout {
-  size_t part_o, part_ml, work, count, total;
+  size_t part_o, part_ml, work, count, work_pre, count_pre, total;
 };
 
-// Workspace: residue partials only when the merge runs in attn_combine (few items), plus the varlen
-// work list.
-Layout workspace_layout(int64_t items, int Hkv, int rows_alloc, bool partials, bool varlen) {
+// Workspace: residue partials only when the merge runs in attn_combine (few items); for varlen, the two
+// work lists and their counts.
+Layout workspace_layout(int64_t items, int Hkv, int rows_alloc, bool partials, bool varlen, int64_t pre_items = 0) {
   Layout L;
   const int64_t cells = partials ? items * Hkv * kResidues * rows_alloc : 0;
   L.part_o = 0;
   L.part_ml = align256(L.part_o + (size_t)cells * kD * sizeof(float));
   L.work = align256(L.part_ml + (size_t)cells * 2 * sizeof(float));
   L.count = align256(L.work + (varlen ? (size_t)items * 2 * sizeof(int32_t) : 0));
-  L.total = align256(L.count + (varlen ? sizeof(int32_t) : 0));
+  L.work_pre = align256(L.count + (varlen ? sizeof(int32_t) : 0));
+  L.count_pre = align256(L.work_pre + (varlen ? (size_t)pre_items * 2 * sizeof(int32_t) : 0));
+  L.total = align256(L.count_pre + (varlen ? sizeof(int32_t) : 0));
   return L;
 }
 
@@ -761,8 +782,18 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
 }
 
 namespace {
-int64_t varlen_items(int32_t num_seqs, int32_t total_q, int P) { return (int64_t)(total_q + P - 1) / P + num_seqs; }
 int varlen_positions(int g) { return max(1, 16 * kVarlenRT / g); }
+// Upper bounds of the two work lists (the launch grids), from host-known sizes only.
+int64_t varlen_items(int32_t num_seqs, int32_t total_q, int P) {
+  const int64_t per_seq = (kResidueMaxQ + P - 1) / P;
+  return std::min<int64_t>((int64_t)num_seqs * per_seq, (int64_t)(total_q + P - 1) / P + num_seqs);
+}
+int prefill_positions(int g) { return kPrefillRows / g; }
+int64_t prefill_items(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q, int g) {
+  if (max_seqlen_q <= kResidueMaxQ) return 0;
+  const int P = prefill_positions(g);
+  return (int64_t)(total_q + P - 1) / P + std::min<int64_t>(num_seqs, total_q / (kResidueMaxQ + 1));
+}
 }  // namespace
 
 extern "C" size_t sd_varlen_workspace_size(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_k, int32_t num_heads,
@@ -770,10 +801,12 @@ extern "C" size_t sd_varlen_workspace_size(int32_t num_seqs, int32_t total_q, in
   if (num_seqs <= 0 || total_q <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
   (void)head_dim;
   (void)max_seqlen_k;
-  const int P = varlen_positions(num_heads / num_kv_heads);
+  const int g = num_heads / num_kv_heads;
+  const int P = varlen_positions(g);
   const int64_t items = varlen_items(num_seqs, total_q, P);
+  const int64_t pre_items = g <= 16 * kVarlenRT ? prefill_items(num_seqs, total_q, INT_MAX, g) : 0;
   const bool partials = residue_waves(items, num_kv_heads, kVarlenRT) < kResidues;
-  return workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true).total;
+  return workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true, pre_items).total;
 }
 
 extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
@@ -809,10 +842,12 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   const int g = num_heads / num_kv_heads;
   const int P = varlen_positions(g);
   const int64_t items = varlen_items(num_seqs, total_q, P);
+  const int64_t pre_items = prefill_items(num_seqs, total_q, max_seqlen_q, g);
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
+  if (pre_items > INT_MAX / 2) return fail(kUnsupported, "%s: too many prefill blocks", who);
   const int waves = residue_waves(items, num_kv_heads, kVarlenRT);
   const bool partials = waves < kResidues;
-  const Layout lay = workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true);
+  const Layout lay = workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true, pre_items);
   if (!workspace || workspace_bytes < lay.total)
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
@@ -846,9 +881,40 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   p.work = work;
   p.work_count = count;
 
+  int32_t* work_pre = (int32_t*)((uint8_t*)workspace + lay.work_pre);
+  int32_t* count_pre = (int32_t*)((uint8_t*)workspace + lay.count_pre);
+
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(varlen_plan, dim3(1), dim3(256), 0, s, cu_seqlens_q, num_seqs, P, work, count, (int32_t)items);
+  hipLaunchKernelGGL(varlen_plan, dim3(1), dim3(kPlanThreads), 0, s, cu_seqlens_q, num_seqs, P, prefill_positions(g),
+                     work, count, (int32_t)items, work_pre, count_pre, (int32_t)pre_items);
   if ((rc = check_launch(who))) return rc;
+  if (pre_items > 0) {
+    PrefillArgs a{};
+    a.q = (const uint16_t*)q;
+    a.q_stride = q_token_stride;
+    a.k = (const uint16_t*)k;
+    a.v = (const uint16_t*)v;
+    a.k_stride = k_token_stride;
+    a.v_stride = v_token_stride;
+    a.block_tables = paged ? block_tables : nullptr;
+    a.table_width = table_width;
+    a.block_size = paged ? block_size : 1;
+    a.num_blocks = num_blocks;
+    a.cu_q = cu_seqlens_q;
+    a.cu_k = cu_seqlens_k;
+    a.work = work_pre;
+    a.work_count = count_pre;
+    a.max_items = (int32_t)pre_items;
+    a.total_q = total_q;
+    a.total_k = total_k;
+    a.Hkv = num_kv_heads;
+    a.g = g;
+    a.P = prefill_positions(g);
+    a.scale_log2 = scale * kLog2e;
+    a.out = (uint16_t*)out;
+    a.out_stride = out_token_stride;
+    if ((rc = launch_prefill(a, s))) return rc;
+  }
   const dim3 grid(1, num_kv_heads, (unsigned)items);
   if (paged)
     launch_rt<kVarlenRT, true, true>(waves, grid, s, p);

@@ -49,4 +49,27 @@ __device__ __forceinline__ void lds_wave_fence() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
+// 2^x with the hardware v_exp_f32.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane exchange with the gfx950 lane-swap instructions instead of LDS permutes.
+// v_permlane16_swap(a, b) exchanges the odd 16-lane rows of a with the even rows of b (v_permlane32_swap:
+// upper half of a with lower half of b), so with a = b = x every lane ends up holding x of itself and of
+// its partner. Written as inline asm because
+// the compiler's builtin does not keep the second register of the pair; the s_nops cover the VALU-write /
+// permlane-read hazard on both sides.
+__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// Two fp32 -> packed bf16 (v_cvt_pk_bf16_f32, round to nearest even).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
 }  // namespace sd

@@ -116,3 +116,27 @@ def test_random_varlen_batches(device):
         out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
         ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
         _check(out, ref, f"random batch {trial}")
+
+
+def test_prefill_rows_chunk_invariant_bitwise(device):
+    """A prefill row's result depends only on its own keys: the same 700-token sequence prefilled as one
+    chunk, as 300 + 400, or beside other sequences gives bitwise equal rows (sequences longer than 16 queries
+    take the prefill kernel, whose reduction order is fixed by key positions)."""
+    Hq, Hkv, D, L = 32, 8, 128, 700
+    kc, vc, tables = paged_cache(device, [L], Hkv, D, seed=12)
+    q = queries(device, L, Hq, D, seed=13)
+
+    def run(lq, lk, qrows, tb):
+        return varlen_attention(qrows, kc, vc, _cu(lq, device), _cu(lk, device), max(lq), max(lk), D ** -0.5, tb)
+
+    whole = run([L], [L], q, tables)
+    first = run([300], [300], q[:300], tables)
+    second = run([400], [L], q[300:], tables)
+    assert torch.equal(whole[:300], first)
+    assert torch.equal(whole[300:], second)
+    # beside a decode sequence and another chunk of the same sequence
+    mixed = run([5, 400, 300], [L, L, 300], torch.cat([q[300:305], q[300:], q[:300]]), tables.repeat(3, 1))
+    assert torch.equal(mixed[5:405], second) and torch.equal(mixed[405:], first)
+    ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), _cu([L], "cpu"), _cu([L], "cpu"), D ** -0.5,
+                                tables.cpu())
+    _check(whole, ref, "700-token prefill")
