@@ -160,17 +160,17 @@ __device__ __forceinline__ float merge_scale(float m_r, float M) {
   return exp2_fast(m_r - (M == -INFINITY ? 0.f : M));
 }
 
-template <int RT, bool kVarlen, bool kPaged, int kWaves>
-__global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes(kWaves)];
+// One (item, KV head h) with the workgroup's kWaves waves, owning residues bx*kWaves .. +kWaves-1; `lds`
+// holds lds_bytes(kWaves). (kCaller only separates the instantiations made from different kernels: the
+// host compilation pass rejects one instantiation reached from two kernels.)
+template <int RT, bool kVarlen, bool kPaged, int kWaves, int kCaller = 0>
+__device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int item, int h, int bx) {
   constexpr bool kMergeHere = kWaves == kResidues;
   constexpr int kStageBytes = stage_bytes(kWaves);
 
-  const int h = blockIdx.y;
-  const int item = blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int residue = blockIdx.x * kWaves + wave;
+  const int residue = bx * kWaves + wave;
   const int lane = tid % kWave;
   const int r16 = lane % 16;  // row (S^T / O^T column) or key (K operand row) owned by this lane
   const int grp = lane / 16;  // 16-lane group: which 8 k-elements / 4 accumulator rows
@@ -483,6 +483,29 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
   }
 }
 
+template <int RT, bool kVarlen, bool kPaged, int kWaves>
+__global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes(kWaves)];
+  attn_body<RT, kVarlen, kPaged, kWaves>(p, lds, blockIdx.z, blockIdx.y, blockIdx.x);
+}
+
+// A varlen call with long query runs: one launch for both work lists, so that the prefill q-blocks (MFMA
+// and latency bound) and the decode / verify items (HBM bound) share the CUs. x < a.max_items: prefill
+// q-block x; otherwise residue item x - a.max_items with all eight residues in the workgroup (merged in
+// LDS, two row tiles).
+constexpr int kMixedLds = lds_bytes(kResidues) > prefill::kLdsBytes ? lds_bytes(kResidues) : prefill::kLdsBytes;
+static_assert(prefill::kThreads == kResidues * kWave, "both halves use 512-thread workgroups");
+
+template <bool kPaged>
+__global__ __launch_bounds__(kResidues * kWave, 2) void mixed_fwd(Params p, PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kMixedLds];
+  const int x = blockIdx.x;
+  if (x < a.max_items)
+    prefill::prefill_body<kPaged>(a, lds, x, blockIdx.y);
+  else
+    attn_body<2, true, kPaged, kResidues, 1>(p, lds, x - a.max_items, blockIdx.y, 0);
+}
+
 // Merges the eight residue partials of every row, in residue order, with the same fma chain as the
 // in-workgroup merge. One wave per row; each lane owns two d values.
 template <bool kVarlen>
@@ -638,6 +661,7 @@ void decode_shape(int n, int g, int* RT, int* P) {
 
 // Varlen prefill / mixed: 2 row tiles (32 rows) per group.
 constexpr int kVarlenRT = 2;
+static_assert(kVarlenRT == 2, "mixed_fwd runs the residue body with two row tiles");
 
 // Waves per workgroup: all eight residues in one workgroup (merge in LDS) when there are enough
 // (item, head) pairs to fill the GPU and the per-wave state allows two waves per SIMD; otherwise fewer
@@ -844,7 +868,7 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   const int64_t items = varlen_items(num_seqs, total_q, P);
   const int64_t pre_items = prefill_items(num_seqs, total_q, max_seqlen_q, g);
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
-  if (pre_items > INT_MAX / 2) return fail(kUnsupported, "%s: too many prefill blocks", who);
+  if (pre_items + items > INT_MAX / 2) return fail(kUnsupported, "%s: too many prefill blocks", who);
   const int waves = residue_waves(items, num_kv_heads, kVarlenRT);
   const bool partials = waves < kResidues;
   const Layout lay = workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true, pre_items);
@@ -913,7 +937,13 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
     a.scale_log2 = scale * kLog2e;
     a.out = (uint16_t*)out;
     a.out_stride = out_token_stride;
-    if ((rc = launch_prefill(a, s))) return rc;
+    // One launch for both lists; its residue items always merge in LDS (no partials, no combine).
+    const dim3 mgrid((unsigned)(pre_items + items), num_kv_heads);
+    if (paged)
+      hipLaunchKernelGGL(mixed_fwd<true>, mgrid, dim3(kResidues * kWave), 0, s, p, a);
+    else
+      hipLaunchKernelGGL(mixed_fwd<false>, mgrid, dim3(kResidues * kWave), 0, s, p, a);
+    return check_launch(who);
   }
   const dim3 grid(1, num_kv_heads, (unsigned)items);
   if (paged)

@@ -72,4 +72,16 @@ __device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ds_read_b64_tr_b16 at LDS byte address `addr` + OFF, as inline asm: with the builtin form the compiler
+// waits for every outstanding vector-memory load (vmcnt(0)) before each read. The caller waits
+// lgkmcnt(0) (tied to the results) before using them.
+template <int OFF>
+__device__ __forceinline__ u32x2 ds_read_tr16(uint32_t addr) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
+
 }  // namespace sd
