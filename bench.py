@@ -21,6 +21,7 @@ import math
 import os
 import sys
 import time
+import types
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 for _p in (ROOT, os.path.join(ROOT, "nano-vllm-spec-decode_amd"), os.path.join(ROOT, "tests")):
@@ -145,9 +146,11 @@ def bench_mixed_attention(dev, steps, warmup, layers=36):
     out = torch.empty(Nq, HQ, D, dtype=torch.bfloat16, device=dev)
 
     def step():
+        owner = types.SimpleNamespace()  # the step's context: layer 1 plans the work lists, the others reuse them
         for kcl, vcl in caches:
             store_kvcache(knew, vnew, kcl, vcl, slots)
-            varlen_attention(q, kcl, vcl, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables, out=out)
+            varlen_attention(q, kcl, vcl, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables, out=out,
+                             plan_owner=owner)
 
     wall, ev = timed(step, steps, warmup)
     t = sum(ev) / len(ev)

@@ -98,6 +98,25 @@ int sd_varlen_attention(const void* q, int64_t q_token_stride, const void* k, in
                         size_t workspace_bytes, void* stream);
 
 /*
+ * Varlen work planning, for callers that run many layers on the same step metadata. sd_varlen_attention
+ * derives its work lists from cu_seqlens_q on the device at every call; sd_varlen_plan writes them into
+ * `workspace` once (it depends only on cu_seqlens_q, num_seqs, total_q, max_seqlen_q and the head counts),
+ * and sd_varlen_attention_planned (same arguments as sd_varlen_attention) then skips that step. The
+ * workspace must hold the plan of exactly these arguments and must not have been written by any other call
+ * in between. No counterpart in the reference (flash-attn plans on the host from max_seqlen alone); it
+ * serves the per-layer loop of nanovllm/engine/model_runner.py:565-589.
+ */
+int sd_varlen_plan(const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q,
+                   int32_t num_heads, int32_t num_kv_heads, void* workspace, size_t workspace_bytes, void* stream);
+int sd_varlen_attention_planned(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
+                                const void* v, int64_t v_token_stride, int64_t total_k, int64_t num_blocks,
+                                int32_t block_size, const int32_t* block_tables, int32_t table_width,
+                                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                                int32_t total_q, int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
+                                int32_t num_kv_heads, int32_t head_dim, float scale, void* out,
+                                int64_t out_token_stride, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Speculative-decoding verifier. Replaces verify_drafts(logits, draft_token_ids, num_drafts,
  * temperatures, draft_logits), nanovllm/layers/sampler.py:28-103, with the reference's internal
  * torch.rand(S, K) and exponential_(1) [S, V] passed in as `uniforms` and `exp_noise`.

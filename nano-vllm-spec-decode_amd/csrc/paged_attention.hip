@@ -818,6 +818,35 @@ int64_t prefill_items(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q, i
   const int P = prefill_positions(g);
   return (int64_t)(total_q + P - 1) / P + std::min<int64_t>(num_seqs, total_q / (kResidueMaxQ + 1));
 }
+
+// Launch shape and workspace layout of a varlen call; a function of the host-known sizes only, shared by
+// the planning and the attention entry points.
+struct VarlenShape {
+  int g, P;
+  int64_t items, pre_items;  // grid sizes (upper bounds) of the residue and prefill work lists
+  int waves;
+  bool partials;
+  Layout lay;
+};
+VarlenShape varlen_shape(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q, int32_t Hq, int32_t Hkv) {
+  VarlenShape v;
+  v.g = Hq / Hkv;
+  v.P = varlen_positions(v.g);
+  v.items = varlen_items(num_seqs, total_q, v.P);
+  v.pre_items = prefill_items(num_seqs, total_q, max_seqlen_q, v.g);
+  v.waves = residue_waves(v.items, Hkv, kVarlenRT);
+  v.partials = v.waves < kResidues;
+  v.lay = workspace_layout(v.items, Hkv, 16 * kVarlenRT, v.partials, true, v.pre_items);
+  return v;
+}
+
+int launch_plan(const int32_t* cu_q, int32_t num_seqs, const VarlenShape& v, void* workspace, hipStream_t s) {
+  hipLaunchKernelGGL(varlen_plan, dim3(1), dim3(kPlanThreads), 0, s, cu_q, num_seqs, v.P, prefill_positions(v.g),
+                     (int32_t*)((uint8_t*)workspace + v.lay.work), (int32_t*)((uint8_t*)workspace + v.lay.count),
+                     (int32_t)v.items, (int32_t*)((uint8_t*)workspace + v.lay.work_pre),
+                     (int32_t*)((uint8_t*)workspace + v.lay.count_pre), (int32_t)v.pre_items);
+  return check_launch("sd_varlen_plan");
+}
 }  // namespace
 
 extern "C" size_t sd_varlen_workspace_size(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_k, int32_t num_heads,
@@ -833,14 +862,13 @@ extern "C" size_t sd_varlen_workspace_size(int32_t num_seqs, int32_t total_q, in
   return workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true, pre_items).total;
 }
 
-extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
-                                   const void* v, int64_t v_token_stride, int64_t total_k, int64_t num_blocks,
-                                   int32_t block_size, const int32_t* block_tables, int32_t table_width,
-                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
-                                   int32_t total_q, int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
-                                   int32_t num_kv_heads, int32_t head_dim, float scale, void* out,
-                                   int64_t out_token_stride, void* workspace, size_t workspace_bytes, void* stream) {
-  const char* who = "sd_varlen_attention";
+namespace {
+int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_stride, const void* k,
+               int64_t k_token_stride, const void* v, int64_t v_token_stride, int64_t total_k, int64_t num_blocks,
+               int32_t block_size, const int32_t* block_tables, int32_t table_width, const int32_t* cu_seqlens_q,
+               const int32_t* cu_seqlens_k, int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q,
+               int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+               void* out, int64_t out_token_stride, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_heads(who, num_heads, num_kv_heads, head_dim);
   if (rc) return rc;
   if (num_seqs < 0 || total_q < 0 || max_seqlen_q < 0 || max_seqlen_k < 0)
@@ -863,15 +891,13 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   if (((uintptr_t)q | (uintptr_t)out | (uintptr_t)k | (uintptr_t)v) % 16 || q_token_stride % 8 ||
       out_token_stride % 8 || k_token_stride % 8 || v_token_stride % 8)
     return fail(kUnsupported, "%s: q / out / k / v must be 16-byte aligned with strides multiple of 8", who);
-  const int g = num_heads / num_kv_heads;
-  const int P = varlen_positions(g);
-  const int64_t items = varlen_items(num_seqs, total_q, P);
-  const int64_t pre_items = prefill_items(num_seqs, total_q, max_seqlen_q, g);
+  const VarlenShape vs = varlen_shape(num_seqs, total_q, max_seqlen_q, num_heads, num_kv_heads);
+  const int g = vs.g, P = vs.P, waves = vs.waves;
+  const int64_t items = vs.items, pre_items = vs.pre_items;
+  const bool partials = vs.partials;
+  const Layout& lay = vs.lay;
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
   if (pre_items + items > INT_MAX / 2) return fail(kUnsupported, "%s: too many prefill blocks", who);
-  const int waves = residue_waves(items, num_kv_heads, kVarlenRT);
-  const bool partials = waves < kResidues;
-  const Layout lay = workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true, pre_items);
   if (!workspace || workspace_bytes < lay.total)
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
@@ -909,9 +935,7 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
   int32_t* count_pre = (int32_t*)((uint8_t*)workspace + lay.count_pre);
 
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(varlen_plan, dim3(1), dim3(kPlanThreads), 0, s, cu_seqlens_q, num_seqs, P, prefill_positions(g),
-                     work, count, (int32_t)items, work_pre, count_pre, (int32_t)pre_items);
-  if ((rc = check_launch(who))) return rc;
+  if (!planned && (rc = launch_plan(cu_seqlens_q, num_seqs, vs, workspace, s))) return rc;
   if (pre_items > 0) {
     PrefillArgs a{};
     a.q = (const uint16_t*)q;
@@ -956,4 +980,49 @@ extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const 
     if ((rc = check_launch(who))) return rc;
   }
   return kOk;
+}
+}  // namespace
+
+extern "C" int sd_varlen_attention(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
+                                   const void* v, int64_t v_token_stride, int64_t total_k, int64_t num_blocks,
+                                   int32_t block_size, const int32_t* block_tables, int32_t table_width,
+                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                                   int32_t total_q, int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
+                                   int32_t num_kv_heads, int32_t head_dim, float scale, void* out,
+                                   int64_t out_token_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  return varlen_run("sd_varlen_attention", false, q, q_token_stride, k, k_token_stride, v, v_token_stride, total_k,
+                    num_blocks, block_size, block_tables, table_width, cu_seqlens_q, cu_seqlens_k, num_seqs, total_q,
+                    max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_dim, scale, out, out_token_stride,
+                    workspace, workspace_bytes, stream);
+}
+
+extern "C" int sd_varlen_attention_planned(const void* q, int64_t q_token_stride, const void* k,
+                                           int64_t k_token_stride, const void* v, int64_t v_token_stride,
+                                           int64_t total_k, int64_t num_blocks, int32_t block_size,
+                                           const int32_t* block_tables, int32_t table_width,
+                                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                                           int32_t total_q, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                                           void* out, int64_t out_token_stride, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  return varlen_run("sd_varlen_attention_planned", true, q, q_token_stride, k, k_token_stride, v, v_token_stride,
+                    total_k, num_blocks, block_size, block_tables, table_width, cu_seqlens_q, cu_seqlens_k, num_seqs,
+                    total_q, max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_dim, scale, out,
+                    out_token_stride, workspace, workspace_bytes, stream);
+}
+
+extern "C" int sd_varlen_plan(const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q,
+                              int32_t num_heads, int32_t num_kv_heads, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  const char* who = "sd_varlen_plan";
+  if (num_seqs < 0 || total_q < 0 || max_seqlen_q < 0 || num_kv_heads <= 0 || num_heads <= 0 ||
+      num_heads % num_kv_heads)
+    return fail(kBadArgument, "%s: bad sizes", who);
+  if (num_seqs == 0 || total_q == 0) return kOk;
+  if (!cu_seqlens_q) return fail(kBadArgument, "%s: null pointer", who);
+  const VarlenShape vs = varlen_shape(num_seqs, total_q, max_seqlen_q, num_heads, num_kv_heads);
+  if (vs.items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)vs.items);
+  if (!workspace || workspace_bytes < vs.lay.total)
+    return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, vs.lay.total);
+  return launch_plan(cu_seqlens_q, num_seqs, vs, workspace, (hipStream_t)stream);
 }

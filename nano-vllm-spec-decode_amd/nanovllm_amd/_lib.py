@@ -30,6 +30,10 @@ SIGNATURES = {
     "sd_varlen_attention": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p,
                                    _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                    _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
+    "sd_varlen_plan": (_i32, [_c_void_p, _i32, _i32, _i32, _i32, _i32, _c_void_p, _size, _c_void_p]),
+    "sd_varlen_attention_planned": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i32,
+                                           _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
+                                           _i32, _f32, _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
     "sd_verify_workspace_size": (_size, [_i32, _i32, _i32, _i32]),
     "sd_verify_drafts": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64,
                                 _c_void_p, _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p, _c_void_p, _size,
@@ -71,14 +75,14 @@ def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-_workspaces: dict[torch.device, list[torch.Tensor]] = {}
+_workspaces: dict[tuple[torch.device, str], list[torch.Tensor]] = {}
 
 
-def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    """A scratch buffer of at least nbytes on `device`, shared by consecutive launches on the current stream.
-    Grows by allocating a bigger buffer; older buffers are kept alive because captured graphs may still
-    point at them."""
-    bufs = _workspaces.setdefault(device, [])
+def workspace(nbytes: int, device: torch.device, tag: str = "") -> torch.Tensor:
+    """A scratch buffer of at least nbytes on `device`, shared by consecutive launches on the current stream
+    (one buffer per `tag`). Grows by allocating a bigger buffer; older buffers are kept alive because
+    captured graphs may still point at them."""
+    bufs = _workspaces.setdefault((device, tag), [])
     if not bufs or bufs[-1].numel() < nbytes:
         size = max(nbytes, 2 * bufs[-1].numel() if bufs else 1 << 20)
         bufs.append(torch.empty(size, dtype=torch.uint8, device=device))

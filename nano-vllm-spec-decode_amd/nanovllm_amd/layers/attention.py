@@ -73,11 +73,23 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     return out
 
 
+# Key of the varlen plan held by the varlen workspace (set by the last sd_varlen_plan call).
+_plan_in_workspace = None
+plan_stats = {"plans": 0, "reuses": 0}
+
+
 def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
                      cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, scale: float,
-                     block_table: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                     block_table: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                     plan_owner: object | None = None) -> torch.Tensor:
     """flash_attn_varlen_func(causal=True) semantics (attention.py:64-70). q [Nq, Hq, D]; k / v are fresh
-    [Nk, Hkv, D] rows, or the paged caches [NB, bs, Hkv, D] when block_table is given."""
+    [Nk, Hkv, D] rows, or the paged caches [NB, bs, Hkv, D] when block_table is given.
+
+    plan_owner: an object that lives exactly as long as this cu_seqlens_q (the step's Context). The work
+    lists derived from cu_seqlens_q are then computed once and reused by every later call with the same
+    owner and sizes, as long as no other plan has replaced them in the varlen workspace. Never reused while
+    a graph is being captured."""
+    global _plan_in_workspace
     Nq, Hq, hd = q.shape
     _require(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
              "varlen_attention: bf16 required")
@@ -100,11 +112,25 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
         NB, bs, W, total_k = 0, 0, 0, kr.size(0)
         ks, vs = kr.stride(0), vr.stride(0)
     nbytes = lib.sd_varlen_workspace_size(nseq, Nq, max_seqlen_k, Hq, Hkv, hd)
-    ws = _lib.workspace(nbytes, q.device)
-    rc = lib.sd_varlen_attention(qr.data_ptr(), qr.stride(0), kr.data_ptr(), ks, vr.data_ptr(), vs, total_k, NB, bs,
-                                 _lib.ptr(block_table), W, cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq,
-                                 max_seqlen_q, max_seqlen_k, Hq, Hkv, hd, scale, out.data_ptr(), out.stride(0),
-                                 ws.data_ptr(), ws.numel(), _lib.stream_of(q.device))
+    ws = _lib.workspace(nbytes, q.device, tag="varlen")
+    stream = _lib.stream_of(q.device)
+    fn = lib.sd_varlen_attention
+    if plan_owner is not None and not torch.cuda.is_current_stream_capturing():
+        key = (id(plan_owner), cu_seqlens_q.data_ptr(), nseq, Nq, max_seqlen_q, Hq, Hkv, ws.data_ptr(), ws.numel())
+        if getattr(plan_owner, "_sd_varlen_plan", None) == key and _plan_in_workspace == key:
+            plan_stats["reuses"] += 1
+        else:
+            _lib.check(lib.sd_varlen_plan(cu_seqlens_q.data_ptr(), nseq, Nq, max_seqlen_q, Hq, Hkv, ws.data_ptr(),
+                                          ws.numel(), stream), "sd_varlen_plan")
+            plan_owner._sd_varlen_plan = key
+            _plan_in_workspace = key
+            plan_stats["plans"] += 1
+        fn = lib.sd_varlen_attention_planned
+    else:
+        _plan_in_workspace = None  # the call below rewrites the work lists
+    rc = fn(qr.data_ptr(), qr.stride(0), kr.data_ptr(), ks, vr.data_ptr(), vs, total_k, NB, bs, _lib.ptr(block_table), W,
+            cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq, max_seqlen_q, max_seqlen_k, Hq, Hkv, hd,
+            scale, out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), stream)
     _lib.check(rc, "sd_varlen_attention")
     return out
 
@@ -129,7 +155,7 @@ class Attention(nn.Module):
             if context.block_tables is not None:    # prefix cache / mixed batching: keys from the paged cache
                 k, v = k_cache, v_cache
             return varlen_attention(q, k, v, context.cu_seqlens_q, context.cu_seqlens_k, context.max_seqlen_q,
-                                    context.max_seqlen_k, self.scale, context.block_tables)
+                                    context.max_seqlen_k, self.scale, context.block_tables, plan_owner=context)
         # decode / verify: every sequence brings the same number of query tokens (1, or 1+k)
         num_seqs = context.context_lens.size(0)
         q = q.reshape(num_seqs, -1, self.num_heads, self.head_dim)

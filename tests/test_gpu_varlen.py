@@ -140,3 +140,34 @@ def test_prefill_rows_chunk_invariant_bitwise(device):
     ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), _cu([L], "cpu"), _cu([L], "cpu"), D ** -0.5,
                                 tables.cpu())
     _check(whole, ref, "700-token prefill")
+
+
+def test_plan_reuse_across_layers(device):
+    """The step's work lists are planned once per owner (the step's Context) and reused by later layers:
+    bitwise equal to unplanned calls; a different owner replans, and so does the first owner afterwards
+    because its plan was replaced in the workspace."""
+    import types
+    from nanovllm_amd.layers import attention as att
+    Hq, Hkv, D = 32, 8, 128
+    lq, lk = mixed_step(3)
+    kc, vc, tables = paged_cache(device, lk, Hkv, D, W=math.ceil(max(lk) / BLOCK), seed=14)
+    q = queries(device, sum(lq), Hq, D, seed=15)
+    cu_q, cu_k = _cu(lq, device), _cu(lk, device)
+    args = (q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
+    ref = varlen_attention(*args)
+    owner = types.SimpleNamespace()
+    plans0, reuses0 = att.plan_stats["plans"], att.plan_stats["reuses"]
+    for _ in range(3):
+        assert torch.equal(varlen_attention(*args, plan_owner=owner), ref)
+    assert att.plan_stats["plans"] - plans0 == 1 and att.plan_stats["reuses"] - reuses0 == 2
+    lq2, lk2 = [5] * 8 + [40], [300] * 8 + [90]
+    kc2, vc2, tb2 = paged_cache(device, lk2, Hkv, D, seed=16)
+    q2 = queries(device, sum(lq2), Hq, D, seed=17)
+    other = types.SimpleNamespace()
+    out2 = varlen_attention(q2, kc2, vc2, _cu(lq2, device), _cu(lk2, device), max(lq2), max(lk2), D ** -0.5, tb2,
+                            plan_owner=other)
+    assert torch.equal(out2, varlen_attention(q2, kc2, vc2, _cu(lq2, device), _cu(lk2, device), max(lq2),
+                                              max(lk2), D ** -0.5, tb2))
+    plans1 = att.plan_stats["plans"]
+    assert torch.equal(varlen_attention(*args, plan_owner=owner), ref)
+    assert att.plan_stats["plans"] == plans1 + 1
