@@ -66,6 +66,28 @@ def timed(fn, steps, warmup):
     return wall, ev
 
 
+def graph_timed(fn, reps=20, replays=5):
+    """Per-call GPU time of fn without host launch overhead: fn is captured `reps` times into one CUDA/HIP
+    graph (after an eager warm-up call) and the graph is replayed between events. Returns seconds per call."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / (reps * replays)
+
+
 def bench_verify_attention(dev, steps, warmup, B=64, k=4, ctx_len=4096, W=33):
     import torch
     from attn_cases import paged_cache, queries
@@ -93,10 +115,9 @@ def bench_store(dev, steps, warmup, N=2048, NB=4096):
     slots[torch.randperm(N, device=dev, generator=g)[:npad]] = -1
     kc = torch.zeros(NB, BLOCK, HKV, D, dtype=torch.bfloat16, device=dev)
     vc = torch.zeros_like(kc)
-    wall, ev = timed(lambda: store_kvcache(key, value, kc, vc, slots), steps, warmup)
+    t = graph_timed(lambda: store_kvcache(key, value, kc, vc, slots))
     nbytes = (N - npad) * 4 * HKV * D * 2 + 4 * N
-    t = sum(ev) / len(ev)
-    return dict(us=t * 1e6, GBs=nbytes / t / 1e9, bytes=nbytes)
+    return dict(us=t * 1e6, GBs=nbytes / t / 1e9, bytes=nbytes, timing="graph replay of 20 calls")
 
 
 def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
@@ -157,8 +178,45 @@ def bench_mixed_attention(dev, steps, warmup, layers=36):
     nd = 48
     flops = sum(4 * HQ * D * (a * (b - a) + a * (a + 1) / 2) for a, b in zip(lq[nd:], lk[nd:]))
     dec_bytes = decode_bytes(lk[:nd], 5)
+    # One layer's attention kernel (work lists planned beforehand), whole step and its prefill chunks alone.
+    layer_s = planned_varlen_time(q, kc, vc, lq, lk, tables)
+    pre = slice(sum(lq[:nd]), Nq)
+    prefill_s = planned_varlen_time(q[pre], kc, vc, lq[nd:], lk[nd:], tables[nd:].contiguous())
     return dict(ms=t * 1e3, tok_s=Nq / t, query_tokens=Nq, decode_seqs=nd, prefill_chunks=len(lq) - nd,
-                prefill_flops_per_layer=flops, decode_bytes_per_layer=dec_bytes)
+                prefill_flops_per_layer=flops, decode_bytes_per_layer=dec_bytes,
+                layer_attention_us=round(layer_s * 1e6, 2),
+                prefill_only_us=round(prefill_s * 1e6, 2),
+                prefill_only_tflops=round(flops / prefill_s / 1e12, 1),
+                prefill_mfma_frac=round(flops / prefill_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                layer_prefill_mfma_frac=round(flops / layer_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4))
+
+
+def planned_varlen_time(q, kc, vc, lq, lk, tables):
+    """Seconds per sd_varlen_attention_planned call (the attention kernel alone; the work lists are planned
+    once outside the timed graph, as the per-layer loop of a step does)."""
+    import numpy as np
+    import torch
+    from nanovllm_amd import _lib
+    dev = q.device
+    lib = _lib.load()
+    Nq, nseq = sum(lq), len(lq)
+    cu_q = torch.tensor([0] + np.cumsum(lq).tolist(), dtype=torch.int32, device=dev)
+    cu_k = torch.tensor([0] + np.cumsum(lk).tolist(), dtype=torch.int32, device=dev)
+    out = torch.empty(Nq, HQ, D, dtype=torch.bfloat16, device=dev)
+    qr = q.contiguous()
+    nbytes = lib.sd_varlen_workspace_size(nseq, Nq, max(lk), HQ, HKV, D)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    stream = lambda: torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.sd_varlen_plan(cu_q.data_ptr(), nseq, Nq, max(lq), HQ, HKV, ws.data_ptr(), nbytes, stream()),
+               "sd_varlen_plan")
+
+    def call():
+        _lib.check(lib.sd_varlen_attention_planned(
+            qr.data_ptr(), qr.stride(0), kc.data_ptr(), HKV * D, vc.data_ptr(), HKV * D, 0, kc.size(0), BLOCK,
+            tables.data_ptr(), tables.size(1), cu_q.data_ptr(), cu_k.data_ptr(), nseq, Nq, max(lq), max(lk), HQ,
+            HKV, D, D ** -0.5, out.data_ptr(), out.stride(0), ws.data_ptr(), nbytes, stream()),
+            "sd_varlen_attention_planned")
+    return graph_timed(call)
 
 
 def cpu_baseline(inputs, min_seconds=10.0, max_reps=8):
