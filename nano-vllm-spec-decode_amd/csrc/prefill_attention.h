@@ -236,12 +236,30 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   float l_part = 0.f;       // this lane's share (16 of the 32 keys per tile) of the row's sum
   const float sl2 = p.scale_log2;
 
+  // Per tile: the eight K operands are read together (one wait), the S^T MFMAs run, then the sixteen
+  // V^T reads are issued before the softmax so that their latency hides behind it.
   auto compute = [&](const uint8_t* kt, const uint8_t* vt, int t, bool need_mask) {
+    const uint32_t kt_addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)kt + k_row;
+    bf16x8 ka[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) ka[st] = ds_read_b128(kt_addr + (((2 * st + half) ^ k_x) * 16));
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(ka[0]), "+v"(ka[1]), "+v"(ka[2]), "+v"(ka[3]), "+v"(ka[4]), "+v"(ka[5]), "+v"(ka[6]),
+                   "+v"(ka[7])
+                 :
+                 : "memory");
     f32x16 s = f32x16{};
 #pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const bf16x8 a = *(const bf16x8*)(kt + k_row + (((2 * st + half) ^ k_x) * 16));
-      s = mfma32(a, qv[st], s);
+    for (int st = 0; st < 8; ++st) s = mfma32(ka[st], qv[st], s);
+    const uint32_t vt_addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)vt + v_base;
+    u32x2 vr[4][4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint32_t a = vt_addr + (((4 * dt) ^ v_x) * 16);
+      vr[dt][0] = ds_read_tr16<0>(a);      // keys 16kk + 4*half + j, kk = 0
+      vr[dt][1] = ds_read_tr16<2048>(a);   //   + 8
+      vr[dt][2] = ds_read_tr16<4096>(a);   // kk = 1
+      vr[dt][3] = ds_read_tr16<6144>(a);
     }
     float x[16];
 #pragma unroll
@@ -282,18 +300,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
       for (int e = 0; e < 4; ++e) w[e] = cvt_bf16x2(x[8 * kk + 2 * e], x[8 * kk + 2 * e + 1]);
       pb[kk] = __builtin_bit_cast(bf16x8, w);
     }
-    // V^T operands of the whole tile (16 transposed reads, 4 per d-tile), then the 8 PV MFMAs.
-    const uint32_t vt_addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)vt + v_base;
-    u32x2 vr[4][4];
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const uint32_t a = vt_addr + (((4 * dt) ^ v_x) * 16);
-      vr[dt][0] = ds_read_tr16<0>(a);      // keys 16kk + 4*half + j, kk = 0
-      vr[dt][1] = ds_read_tr16<2048>(a);   //   + 8
-      vr[dt][2] = ds_read_tr16<4096>(a);   // kk = 1
-      vr[dt][3] = ds_read_tr16<6144>(a);
-    }
-    // The reads' results pass through the wait, so no MFMA can be scheduled before it.
+    // The V^T reads' results pass through the wait, so no MFMA can be scheduled before it.
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(vr[0][0]), "+v"(vr[0][1]), "+v"(vr[0][2]), "+v"(vr[0][3]), "+v"(vr[1][0]), "+v"(vr[1][1]),
                    "+v"(vr[1][2]), "+v"(vr[1][3]), "+v"(vr[2][0]), "+v"(vr[2][1]), "+v"(vr[2][2]), "+v"(vr[2][3]),

@@ -84,4 +84,11 @@ __device__ __forceinline__ u32x2 ds_read_tr16(uint32_t addr) {
   return r;
 }
 
+// ds_read_b128 at LDS byte address `addr`, as inline asm (batched reads with one tied wait; see above).
+__device__ __forceinline__ bf16x8 ds_read_b128(uint32_t addr) {
+  bf16x8 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+
 }  // namespace sd
