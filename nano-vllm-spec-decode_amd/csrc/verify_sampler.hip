@@ -1,17 +1,19 @@
 // Speculative-decoding verifier and token sampler over the full vocabulary (replaces verify_drafts and
 // Sampler.forward, nanovllm/layers/sampler.py:5-103).
 //
-// Four small kernels, all HBM-streaming over [rows, vocab] tables:
-//   1. row_stats      (row, chunk): per 4096-entry chunk of every target row: first argmax of the raw
-//                     logits; for rows with temperature != 0 also max and sum(exp(x - max)) of x = l / T
-//                     (target rows and, when given, draft rows).
-//   2. verify_decide  (seq): merges chunk stats in chunk order (argmax, logsumexp), applies the accept rule
+// Three kernels, two of them HBM-streaming over [rows, vocab] tables. A row is cut into at most
+// kSpans contiguous spans (a multiple of 4 entries each, none empty); a 256-thread workgroup streams one
+// span with 4-entry loads (16 B for fp32, 8 B for bf16; scalar loads when the rows are not aligned).
+//   1. row_stats      (row, span): first argmax of the raw logits of target rows; for rows with temperature
+//                     != 0 also max and sum(exp(x - max)) of x = l / T (target rows and, when given, draft
+//                     rows), kept per thread online and combined in a fixed order.
+//   2. verify_decide  (seq): merges span stats in span order (argmax, logsumexp), applies the accept rule
 //                     u * q(d) < p(d) (or top1 == d for greedy rows) to the leading run of real guesses,
 //                     writes num_accepted and, for greedy rows, next_token.
-//   3. verify_resample(seq, chunk): random rows only: per chunk, the first argmax of p / max(E, 1e-10) and
-//                     of residual / max(E, 1e-10) with p = softmax(row a / T), residual = max(p - q, 0)
-//                     (or p with the rejected n-gram guess zeroed), and whether any residual is positive.
-//   4. verify_finish  (seq): merges the chunk candidates in order and picks the token.
+//   3. verify_resample(seq, span): random rows only: the first argmax of p / max(E, 1e-10) and of
+//                     residual / max(E, 1e-10) with p = softmax(row a / T), residual = max(p - q, 0) (or p
+//                     with the rejected n-gram guess zeroed), and whether any residual is positive; the last
+//                     span workgroup of a sequence merges the span candidates in order and picks the token.
 // Every reduction has a fixed order, so results are deterministic; ties resolve to the first index (and a
 // NaN counts as the largest value), as torch.argmax does.
 #include <math.h>
@@ -22,7 +24,7 @@
 namespace sd {
 namespace {
 
-constexpr int kChunk = 4096;      // vocabulary entries per workgroup
+constexpr int kSpans = 8;         // most spans per row (workgroups per row)
 constexpr int kThreads = 256;
 
 struct RowStat {                  // per (row, chunk)
@@ -65,6 +67,31 @@ __device__ __forceinline__ float load_logit(const void* base, int64_t idx) {
   return bf16_bits_to_f32(((const uint16_t*)base)[idx]);
 }
 
+// Entries idx .. idx+3 (idx a multiple of 4; the row 16-byte aligned for fp32, 8-byte for bf16).
+template <int DT>
+__device__ __forceinline__ float4 load_logit4(const void* base, int64_t idx) {
+  if (DT == SD_DTYPE_F32) return *(const float4*)((const float*)base + idx);
+  const uint2 w = *(const uint2*)((const uint16_t*)base + idx);
+  return make_float4(__builtin_bit_cast(float, w.x << 16), __builtin_bit_cast(float, w.x & 0xffff0000u),
+                     __builtin_bit_cast(float, w.y << 16), __builtin_bit_cast(float, w.y & 0xffff0000u));
+}
+
+// Online (max, sum of exp(x - max)) of one thread's entries; an infinite or empty max uses 0 as the shift.
+struct OnlineSum {
+  float m = -INFINITY, s = 0.f;
+  __device__ __forceinline__ float shift() const { return fabsf(m) == INFINITY ? 0.f : m; }
+  __device__ __forceinline__ void add4(float x0, float x1, float x2, float x3) {
+    const float ml = fmaxf(fmaxf(x0, x1), fmaxf(x2, x3));
+    if (ml > m) {
+      const float old = shift();
+      m = ml;
+      s *= expf(old - shift());
+    }
+    const float sh = shift();
+    s += expf(x0 - sh) + expf(x1 - sh) + expf(x2 - sh) + expf(x3 - sh);
+  }
+};
+
 // Block-wide reductions over 256 threads (4 waves) in a fixed order.
 __device__ __forceinline__ float block_max(float v, float* sh) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
@@ -82,6 +109,35 @@ __device__ __forceinline__ float block_sum(float v, float* sh) {
   if (threadIdx.x % kWave == 0) sh[w] = v;
   __syncthreads();
   return ((sh[0] + sh[1]) + sh[2]) + sh[3];
+}
+
+// Combines the threads' (max, sum) pairs in a fixed order: lanes by xor-shuffle, then waves 0..3.
+__device__ __forceinline__ void combine_online(OnlineSum& o, float* sh) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float om = __shfl_xor(o.m, off), os = __shfl_xor(o.s, off);
+    const float M = fmaxf(o.m, om);
+    const float sh_ = fabsf(M) == INFINITY ? 0.f : M;
+    const float a = fabsf(o.m) == INFINITY ? 0.f : o.m, b = fabsf(om) == INFINITY ? 0.f : om;
+    o.s = o.s * expf(a - sh_) + os * expf(b - sh_);
+    o.m = M;
+  }
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) {
+    sh[2 * w] = o.m;
+    sh[2 * w + 1] = o.s;
+  }
+  __syncthreads();
+  float M = -INFINITY;
+  for (int k = 0; k < 4; ++k) M = fmaxf(M, sh[2 * k]);
+  const float shM = fabsf(M) == INFINITY ? 0.f : M;
+  float S = 0.f;
+  for (int k = 0; k < 4; ++k) {
+    const float mk = sh[2 * k];
+    S += sh[2 * k + 1] * expf((fabsf(mk) == INFINITY ? 0.f : mk) - shM);
+  }
+  o.m = M;
+  o.s = S;
 }
 
 __device__ __forceinline__ void block_argmax(float& v, int& i, float* shv, int* shi) {
@@ -119,17 +175,18 @@ struct VParams {
   int64_t draft_stride;
   const float* uniforms;          // [S, K]
   const float* noise;             // [S, V]
-  int32_t S, K, V, nchunk;
+  int32_t S, K, V, nchunk, span;  // nchunk spans of `span` entries (the last may be shorter)
   int64_t* out_a;
   int64_t* out_next;
   RowStat* stats;                 // [(S*(K+1) + S*K) rows][nchunk]
   SeqInfo* info;                  // [S]
   Cand* cand;                     // [S][nchunk]
+  int32_t* done;                  // [S] finished resample workgroups
 };
 
-template <int DT, int DDT>
+template <int DT, int DDT, bool kVec>
 __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
-  __shared__ float shf[4];
+  __shared__ float shf[8];
   __shared__ int shi[4];
   const int row = blockIdx.x;
   const int chunk = blockIdx.y;
@@ -148,24 +205,38 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
     base = DDT == SD_DTYPE_F32 ? (const void*)((const float*)p.draft_logits + dr * p.draft_stride)
                                : (const void*)((const uint16_t*)p.draft_logits + dr * p.draft_stride);
   }
-  const int v0 = chunk * kChunk;
-  const int v1 = min(v0 + kChunk, p.V);
-  constexpr int kPer = kChunk / kThreads;  // 16 entries per thread, strided by kThreads
-  float x[kPer];
+  const int v0 = chunk * p.span;
+  const int v1 = min(v0 + p.span, p.V);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int v = v0 + e * kThreads + threadIdx.x;
-    if (v < v1) {
-      const float raw = is_target ? load_logit<DT>(base, v) : load_logit<DDT>(base, v);
-      if (is_target && better(raw, v, bv, bi)) {
-        bv = raw;
-        bi = v;
-      }
-      x[e] = raw / T;
+  OnlineSum os;
+  auto visit = [&](float raw, int v) {  // scalar entry
+    if (is_target && better(raw, v, bv, bi)) {
+      bv = raw;
+      bi = v;
+    }
+  };
+  for (int v = v0 + 4 * threadIdx.x; v < v1; v += 4 * kThreads) {
+    float r[4];
+    if (kVec && v + 4 <= v1) {
+      const float4 q4 = is_target ? load_logit4<DT>(base, v) : load_logit4<DDT>(base, v);
+      r[0] = q4.x;
+      r[1] = q4.y;
+      r[2] = q4.z;
+      r[3] = q4.w;
     } else {
-      x[e] = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        r[e] = v + e < v1 ? (is_target ? load_logit<DT>(base, v + e) : load_logit<DDT>(base, v + e)) : -INFINITY;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (v + e < v1) visit(r[e], v + e);
+    if (random) {
+      float x[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = v + e < v1 ? (T == 1.f ? r[e] : r[e] / T) : -INFINITY;  // x / 1 == x
+      os.add4(x[0], x[1], x[2], x[3]);
     }
   }
   RowStat st;
@@ -175,17 +246,9 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
   st.best = bv;
   st.best_idx = bi;
   if (random) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) mx = fmaxf(mx, x[e]);
-    mx = block_max(mx, shf);
-    const float m_use = fabsf(mx) == INFINITY ? 0.f : mx;
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) s += expf(x[e] - m_use);
-    s = block_sum(s, shf);
-    st.max_x = m_use;
-    st.sum = s;
+    combine_online(os, shf);
+    st.max_x = fabsf(os.m) == INFINITY ? 0.f : os.m;
+    st.sum = os.s;
   }
   if (threadIdx.x == 0) p.stats[(int64_t)row * p.nchunk + chunk] = st;
 }
@@ -236,10 +299,10 @@ __global__ __launch_bounds__(64) void verify_decide(VParams p) {
     }
   }
   __syncthreads();
-  if (lane != 0) return;
+  // Each lane evaluates one guess (the scattered loads run in parallel), lane 0 takes the leading run.
+  __shared__ int accj[64];
   const int64_t nd = p.num_drafts ? p.num_drafts[seq] : 0;
-  int a = 0;
-  for (int j = 0; j < K; ++j) {
+  for (int j = lane; j < K; j += 64) {
     const int64_t d = p.drafts[(int64_t)seq * K + j];
     bool acc = false;
     if (j < nd && d >= 0 && d < p.V) {
@@ -262,10 +325,14 @@ __global__ __launch_bounds__(64) void verify_decide(VParams p) {
         acc = u * qd < pd;
       }
     }
-    if (!acc) break;
-    ++a;
+    accj[j] = acc ? 1 : 0;
   }
+  __syncthreads();
+  if (lane != 0) return;
+  int a = 0;
+  while (a < K && accj[a]) ++a;
   p.out_a[seq] = a;
+  p.done[seq] = 0;
   SeqInfo info{};
   info.a = a;
   info.random = random ? 1 : 0;
@@ -291,73 +358,8 @@ __global__ __launch_bounds__(64) void verify_decide(VParams p) {
   p.info[seq] = info;
 }
 
-template <int DT, int DDT>
-__global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
-  __shared__ float shf[4];
-  __shared__ int shi[4];
-  const int seq = blockIdx.x;
-  const int chunk = blockIdx.y;
-  const SeqInfo info = p.info[seq];
-  if (!info.random) return;
-  const float T = p.temps[seq];
-  const int K = p.K;
-  const int64_t trow = (int64_t)seq * (K + 1) + info.a;
-  const int64_t drow = (int64_t)seq * K + min(info.a, K - 1);
-  const float* noise = p.noise ? p.noise + (int64_t)seq * p.V : nullptr;  // missing noise: E = 1
-  const int v0 = chunk * kChunk;
-  const int v1 = min(v0 + kChunk, p.V);
-  constexpr int kPer = kChunk / kThreads;
-  float pv = -INFINITY, rv = -INFINITY;
-  int pi = 0x7fffffff, ri = 0x7fffffff;
-  int any_res = 0;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int v = v0 + e * kThreads + threadIdx.x;
-    if (v >= v1) continue;
-    const float l = (DT == SD_DTYPE_F32) ? ((const float*)p.logits)[trow * p.logits_stride + v]
-                                         : bf16_bits_to_f32(((const uint16_t*)p.logits)[trow * p.logits_stride + v]);
-    float prob = expf(l / T - info.Ma) / info.Sa;
-    const float E = noise ? fmaxf(noise[v], 1e-10f) : 1.f;
-    if (info.resid_mode == 1 && info.rejected && v == info.guess) prob = 0.f;
-    const float sp = prob / E;
-    if (better(sp, v, pv, pi)) {
-      pv = sp;
-      pi = v;
-    }
-    if (info.resid_mode == 2) {
-      const float ld = (DDT == SD_DTYPE_F32)
-                           ? ((const float*)p.draft_logits)[drow * p.draft_stride + v]
-                           : bf16_bits_to_f32(((const uint16_t*)p.draft_logits)[drow * p.draft_stride + v]);
-      const float q = expf(ld / T - info.Md) / info.Sd;
-      const float res = fmaxf(prob - q, 0.f);
-      any_res |= res > 0.f;
-      const float sr = res / E;
-      if (better(sr, v, rv, ri)) {
-        rv = sr;
-        ri = v;
-      }
-    }
-  }
-  block_argmax(pv, pi, shf, shi);
-  Cand c{};
-  c.p_val = pv;
-  c.p_idx = pi;
-  if (info.resid_mode == 2) {
-    block_argmax(rv, ri, shf, shi);
-    any_res = __syncthreads_or(any_res);
-  }
-  c.r_val = rv;
-  c.r_idx = ri;
-  c.any_res = any_res;
-  if (threadIdx.x == 0) p.cand[(int64_t)seq * p.nchunk + chunk] = c;
-}
-
-__global__ __launch_bounds__(64) void verify_finish(VParams p) {
-  const int seq = blockIdx.x * 64 + threadIdx.x;
-  if (seq >= p.S) return;
-  const SeqInfo info = p.info[seq];
-  if (!info.random) return;
-  const Cand* c = p.cand + (int64_t)seq * p.nchunk;
+__device__ void finish_seq(const VParams& p, int seq, const SeqInfo& info) {
+  const volatile Cand* c = p.cand + (int64_t)seq * p.nchunk;
   float pv = c[0].p_val, rv = c[0].r_val;
   int pi = c[0].p_idx, ri = c[0].r_idx;
   int any_res = c[0].any_res;
@@ -376,35 +378,138 @@ __global__ __launch_bounds__(64) void verify_finish(VParams p) {
   p.out_next[seq] = use_res ? ri : pi;
 }
 
+template <int DT, int DDT, bool kVec>
+__global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
+  __shared__ float shf[4];
+  __shared__ int shi[4];
+  const int seq = blockIdx.x;
+  const int chunk = blockIdx.y;
+  const SeqInfo info = p.info[seq];
+  if (!info.random) return;
+  const float T = p.temps[seq];
+  const int K = p.K;
+  const int64_t trow = (int64_t)seq * (K + 1) + info.a;
+  const int64_t drow = (int64_t)seq * K + min(info.a, K - 1);
+  const void* tbase = DT == SD_DTYPE_F32 ? (const void*)((const float*)p.logits + trow * p.logits_stride)
+                                         : (const void*)((const uint16_t*)p.logits + trow * p.logits_stride);
+  const void* dbase = nullptr;
+  if (info.resid_mode == 2)
+    dbase = DDT == SD_DTYPE_F32 ? (const void*)((const float*)p.draft_logits + drow * p.draft_stride)
+                                : (const void*)((const uint16_t*)p.draft_logits + drow * p.draft_stride);
+  const float* noise = p.noise ? p.noise + (int64_t)seq * p.V : nullptr;  // missing noise: E = 1
+  const int v0 = chunk * p.span;
+  const int v1 = min(v0 + p.span, p.V);
+  float pv = -INFINITY, rv = -INFINITY;
+  int pi = 0x7fffffff, ri = 0x7fffffff;
+  int any_res = 0;
+  for (int v = v0 + 4 * threadIdx.x; v < v1; v += 4 * kThreads) {
+    const bool full = kVec && v + 4 <= v1;
+    float l[4], E[4], ld[4];
+    if (full) {
+      const float4 t4 = load_logit4<DT>(tbase, v);
+      l[0] = t4.x, l[1] = t4.y, l[2] = t4.z, l[3] = t4.w;
+      if (noise) {
+        const float4 e4 = *(const float4*)(noise + v);
+        E[0] = e4.x, E[1] = e4.y, E[2] = e4.z, E[3] = e4.w;
+      }
+      if (dbase) {
+        const float4 d4 = load_logit4<DDT>(dbase, v);
+        ld[0] = d4.x, ld[1] = d4.y, ld[2] = d4.z, ld[3] = d4.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool in = v + e < v1;
+        l[e] = in ? load_logit<DT>(tbase, v + e) : 0.f;
+        if (noise) E[e] = in ? noise[v + e] : 1.f;
+        if (dbase) ld[e] = in ? load_logit<DDT>(dbase, v + e) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = v + e;
+      if (idx >= v1) continue;
+      float prob = expf((T == 1.f ? l[e] : l[e] / T) - info.Ma) / info.Sa;  // divided, as softmax does
+      const float Ee = noise ? fmaxf(E[e], 1e-10f) : 1.f;
+      if (info.resid_mode == 1 && info.rejected && idx == info.guess) prob = 0.f;
+      const float sp = prob / Ee;
+      if (better(sp, idx, pv, pi)) {
+        pv = sp;
+        pi = idx;
+      }
+      if (dbase) {
+        const float q = expf((T == 1.f ? ld[e] : ld[e] / T) - info.Md) / info.Sd;
+        const float res = fmaxf(prob - q, 0.f);
+        any_res |= res > 0.f;
+        const float sr = res / Ee;
+        if (better(sr, idx, rv, ri)) {
+          rv = sr;
+          ri = idx;
+        }
+      }
+    }
+  }
+  block_argmax(pv, pi, shf, shi);
+  Cand c{};
+  c.p_val = pv;
+  c.p_idx = pi;
+  if (info.resid_mode == 2) {
+    block_argmax(rv, ri, shf, shi);
+    any_res = __syncthreads_or(any_res);
+  }
+  c.r_val = rv;
+  c.r_idx = ri;
+  c.any_res = any_res;
+  // The last workgroup of the sequence to finish merges the span candidates (counter zeroed by
+  // verify_decide).
+  __shared__ int last;
+  if (threadIdx.x == 0) {
+    p.cand[(int64_t)seq * p.nchunk + chunk] = c;
+    __threadfence();
+    last = atomicAdd(&p.done[seq], 1) == p.nchunk - 1;
+  }
+  __syncthreads();
+  if (!last || threadIdx.x != 0) return;
+  __threadfence();
+  finish_seq(p, seq, info);
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct VLayout {
-  size_t stats, info, cand, total;
+  size_t stats, info, cand, done, total;
 };
 
+// Spans of a row: at most kSpans, a multiple of 4 entries each, none empty.
+void row_spans(int V, int* nchunk, int* span) {
+  const int n0 = min(kSpans, (V + 3) / 4);
+  *span = (((V + n0 - 1) / n0) + 3) / 4 * 4;
+  *nchunk = (V + *span - 1) / *span;
+}
+
 VLayout verify_layout(int S, int K, int V, bool draft) {
-  const int nchunk = (V + kChunk - 1) / kChunk;
+  int nchunk, span;
+  row_spans(V, &nchunk, &span);
   const int64_t rows = (int64_t)S * (K + 1) + (draft ? (int64_t)S * K : 0);
   VLayout L;
   L.stats = 0;
   L.info = align256((size_t)rows * nchunk * sizeof(RowStat));
   L.cand = align256(L.info + (size_t)S * sizeof(SeqInfo));
-  L.total = align256(L.cand + (size_t)S * nchunk * sizeof(Cand));
+  L.done = align256(L.cand + (size_t)S * nchunk * sizeof(Cand));
+  L.total = align256(L.done + (size_t)S * sizeof(int32_t));
   return L;
 }
 
-template <int DT, int DDT>
+template <int DT, int DDT, bool kVec>
 int launch_all(const VParams& p, hipStream_t s, bool draft) {
   int rc;
   const int rows = p.S * (p.K + 1) + (draft ? p.S * p.K : 0);
-  hipLaunchKernelGGL((row_stats<DT, DDT>), dim3(rows, p.nchunk), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL((row_stats<DT, DDT, kVec>), dim3(rows, p.nchunk), dim3(kThreads), 0, s, p);
   if ((rc = check_launch("row_stats"))) return rc;
   hipLaunchKernelGGL((verify_decide<DT, DDT>), dim3(p.S), dim3(64), 0, s, p);
   if ((rc = check_launch("verify_decide"))) return rc;
-  hipLaunchKernelGGL((verify_resample<DT, DDT>), dim3(p.S, p.nchunk), dim3(kThreads), 0, s, p);
-  if ((rc = check_launch("verify_resample"))) return rc;
-  hipLaunchKernelGGL(verify_finish, dim3((p.S + 63) / 64), dim3(64), 0, s, p);
-  return check_launch("verify_finish");
+  hipLaunchKernelGGL((verify_resample<DT, DDT, kVec>), dim3(p.S, p.nchunk), dim3(kThreads), 0, s, p);
+  return check_launch("verify_resample");
 }
 
 int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
@@ -423,7 +528,7 @@ int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_
     return fail(kUnsupported, "%s: draft dtype %d not supported", who, draft_dtype);
   if (logits_row_stride < V || (draft_logits && draft_row_stride < V))
     return fail(kBadArgument, "%s: row stride smaller than vocab", who);
-  if ((int64_t)S * (K + 1) + (draft_logits ? (int64_t)S * K : 0) > 0x7fffffff || (V + kChunk - 1) / kChunk > 65535)
+  if ((int64_t)S * (K + 1) + (draft_logits ? (int64_t)S * K : 0) > 0x7fffffff || S > 0x7fffffff)
     return fail(kUnsupported, "%s: too many rows or vocabulary entries for one launch", who);
   const bool draft = draft_logits != nullptr && K > 0;
   const VLayout lay = verify_layout(S, K, V, draft);
@@ -442,19 +547,34 @@ int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_
   p.S = S;
   p.K = K;
   p.V = V;
-  p.nchunk = (V + kChunk - 1) / kChunk;
+  row_spans(V, &p.nchunk, &p.span);
   p.out_a = out_a;
   p.out_next = out_next;
   p.stats = (RowStat*)((uint8_t*)workspace + lay.stats);
   p.info = (SeqInfo*)((uint8_t*)workspace + lay.info);
   p.cand = (Cand*)((uint8_t*)workspace + lay.cand);
+  p.done = (int32_t*)((uint8_t*)workspace + lay.done);
   hipStream_t s = (hipStream_t)stream;
   const bool lf = logits_dtype == SD_DTYPE_F32;
   const bool df = draft && draft_dtype == SD_DTYPE_F32;
-  if (lf && df) return launch_all<SD_DTYPE_F32, SD_DTYPE_F32>(p, s, draft);
-  if (lf) return launch_all<SD_DTYPE_F32, SD_DTYPE_BF16>(p, s, draft);
-  if (df) return launch_all<SD_DTYPE_BF16, SD_DTYPE_F32>(p, s, draft);
-  return launch_all<SD_DTYPE_BF16, SD_DTYPE_BF16>(p, s, draft);
+  // 4-entry loads need every row (and the noise rows) aligned to 4 entries' bytes.
+  auto aligned = [](const void* ptr, int64_t stride, int elem) {
+    const int64_t a = 4 * elem;
+    return (uintptr_t)ptr % a == 0 && (stride * elem) % a == 0;
+  };
+  const bool vec = aligned(logits, logits_row_stride, lf ? 4 : 2) &&
+                   (!draft || aligned(draft_logits, draft_row_stride, df ? 4 : 2)) &&
+                   (!noise || aligned(noise, V, 4));
+  if (vec) {
+    if (lf && df) return launch_all<SD_DTYPE_F32, SD_DTYPE_F32, true>(p, s, draft);
+    if (lf) return launch_all<SD_DTYPE_F32, SD_DTYPE_BF16, true>(p, s, draft);
+    if (df) return launch_all<SD_DTYPE_BF16, SD_DTYPE_F32, true>(p, s, draft);
+    return launch_all<SD_DTYPE_BF16, SD_DTYPE_BF16, true>(p, s, draft);
+  }
+  if (lf && df) return launch_all<SD_DTYPE_F32, SD_DTYPE_F32, false>(p, s, draft);
+  if (lf) return launch_all<SD_DTYPE_F32, SD_DTYPE_BF16, false>(p, s, draft);
+  if (df) return launch_all<SD_DTYPE_BF16, SD_DTYPE_F32, false>(p, s, draft);
+  return launch_all<SD_DTYPE_BF16, SD_DTYPE_BF16, false>(p, s, draft);
 }
 
 }  // namespace
