@@ -206,8 +206,8 @@ def planned_varlen_time(q, kc, vc, lq, lk, tables):
     nbytes = lib.sd_varlen_workspace_size(nseq, Nq, max(lk), HQ, HKV, D)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     stream = lambda: torch.cuda.current_stream().cuda_stream
-    _lib.check(lib.sd_varlen_plan(cu_q.data_ptr(), nseq, Nq, max(lq), HQ, HKV, ws.data_ptr(), nbytes, stream()),
-               "sd_varlen_plan")
+    _lib.check(lib.sd_varlen_plan(cu_q.data_ptr(), cu_k.data_ptr(), nseq, Nq, max(lq), HQ, HKV, ws.data_ptr(), nbytes,
+                                  stream()), "sd_varlen_plan")
 
     def call():
         _lib.check(lib.sd_varlen_attention_planned(

@@ -99,15 +99,18 @@ int sd_varlen_attention(const void* q, int64_t q_token_stride, const void* k, in
 
 /*
  * Varlen work planning, for callers that run many layers on the same step metadata. sd_varlen_attention
- * derives its work lists from cu_seqlens_q on the device at every call; sd_varlen_plan writes them into
- * `workspace` once (it depends only on cu_seqlens_q, num_seqs, total_q, max_seqlen_q and the head counts),
- * and sd_varlen_attention_planned (same arguments as sd_varlen_attention) then skips that step. The
- * workspace must hold the plan of exactly these arguments and must not have been written by any other call
- * in between. No counterpart in the reference (flash-attn plans on the host from max_seqlen alone); it
- * serves the per-layer loop of nanovllm/engine/model_runner.py:565-589.
+ * derives its work lists from cu_seqlens_q / cu_seqlens_k on the device at every call; sd_varlen_plan writes
+ * them into `workspace` once (they depend only on cu_seqlens_q, cu_seqlens_k, num_seqs, total_q,
+ * max_seqlen_q and the head counts), and sd_varlen_attention_planned (same arguments as sd_varlen_attention)
+ * then skips that step. The workspace must hold the plan of exactly these arguments and must not have been
+ * written by any other call in between. The lists put the sequences with the most keys first (up to 1024
+ * sequences; index order beyond), which changes the order work is dispatched in, never a row's result.
+ * No counterpart in the reference (flash-attn plans on the host from max_seqlen alone); it serves the
+ * per-layer loop of nanovllm/engine/model_runner.py:565-589.
  */
-int sd_varlen_plan(const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q,
-                   int32_t num_heads, int32_t num_kv_heads, void* workspace, size_t workspace_bytes, void* stream);
+int sd_varlen_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs, int32_t total_q,
+                   int32_t max_seqlen_q, int32_t num_heads, int32_t num_kv_heads, void* workspace,
+                   size_t workspace_bytes, void* stream);
 int sd_varlen_attention_planned(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
                                 const void* v, int64_t v_token_stride, int64_t total_k, int64_t num_blocks,
                                 int32_t block_size, const int32_t* block_tables, int32_t table_width,

@@ -499,11 +499,12 @@ static_assert(prefill::kThreads == kResidues * kWave, "both halves use 512-threa
 template <bool kPaged>
 __global__ __launch_bounds__(kResidues * kWave, 2) void mixed_fwd(Params p, PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kMixedLds];
-  const int x = blockIdx.x;
+  const int h = blockIdx.x % a.Hkv;
+  const int x = blockIdx.x / a.Hkv;
   if (x < a.max_items)
-    prefill::prefill_body<kPaged>(a, lds, x, blockIdx.y);
+    prefill::prefill_body<kPaged>(a, lds, x, h);
   else
-    attn_body<2, true, kPaged, kResidues, 1>(p, lds, x - a.max_items, blockIdx.y, 0);
+    attn_body<2, true, kPaged, kResidues, 1>(p, lds, x - a.max_items, h, 0);
 }
 
 // Merges the eight residue partials of every row, in residue order, with the same fma chain as the
@@ -551,8 +552,11 @@ __global__ __launch_bounds__(256) void attn_combine(Params p) {
 
 // Varlen work lists. A sequence with 1..kResidueMaxQ queries contributes ceil(Lq / P_res) (sequence, group)
 // items of the residue kernel; a longer one contributes ceil(Lq / P_pre) (sequence, q-block) items of the
-// prefill kernel, its last q-block (the one that sees the most keys) first. One 1024-thread workgroup: each
-// pass scans 1024 sequences (wave prefix sums, then the wave totals).
+// prefill kernel, its last q-block (the one that sees the most keys) first. With at most kPlanThreads
+// sequences, the sequences are taken in decreasing order of key count (ties by index; a bitonic sort in
+// LDS), so that the longest work items are dispatched first and the short ones fill the tail; with more,
+// in index order. One 1024-thread workgroup: each pass takes 1024 sequences (wave prefix sums, then the wave
+// totals). The order changes only which workgroup computes an item, never an item's arithmetic.
 constexpr int kPlanThreads = 1024;
 __device__ __forceinline__ int wave_inclusive_sum(int x, int lane) {
 #pragma unroll
@@ -563,21 +567,50 @@ __device__ __forceinline__ int wave_inclusive_sum(int x, int lane) {
   return x;
 }
 
-__global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __restrict__ cu_q, int32_t num_seqs,
+__global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __restrict__ cu_q,
+                                                            const int32_t* __restrict__ cu_k, int32_t num_seqs,
                                                             int32_t P_res, int32_t P_pre,
                                                             int32_t* __restrict__ work_res, int32_t* __restrict__ count_res,
                                                             int32_t max_res, int32_t* __restrict__ work_pre,
                                                             int32_t* __restrict__ count_pre, int32_t max_pre) {
   constexpr int kPlanWaves = kPlanThreads / kWave;
+  static_assert(kPlanThreads == 1024, "sort keys hold a 10-bit sequence index");
   __shared__ int32_t wsum[2][kPlanWaves];
   __shared__ int32_t carry[2];
+  __shared__ uint32_t keys[kPlanThreads];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const bool sorted = num_seqs <= kPlanThreads;
   if (tid < 2) carry[tid] = 0;
+  if (sorted) {
+    // key = (2^20 - 1 - key tiles) << 10 | sequence: ascending keys = descending work, then index order.
+    uint32_t key = 0xFFFFFFFFu;
+    if (tid < num_seqs) {
+      const int Lk = max(cu_k[tid + 1] - cu_k[tid], 0);
+      const uint32_t tiles = min((uint32_t)(Lk + kTile - 1) / kTile, (1u << 20) - 1);
+      key = (((1u << 20) - 1 - tiles) << 10) | (uint32_t)tid;
+    }
+    keys[tid] = key;
+    __syncthreads();
+    for (int k = 2; k <= kPlanThreads; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const int other = tid ^ j;
+        if (other > tid) {
+          const uint32_t a = keys[tid], b = keys[other];
+          if ((a > b) == ((tid & k) == 0)) {
+            keys[tid] = b;
+            keys[other] = a;
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
   __syncthreads();
   for (int base = 0; base < num_seqs; base += kPlanThreads) {
-    const int s = base + tid;
+    const int idx = base + tid;
+    const int s = sorted ? (int)(keys[tid] & 1023u) : idx;
     int Lq = 0;
-    if (s < num_seqs) Lq = max(cu_q[s + 1] - cu_q[s], 0);
+    if (idx < num_seqs) Lq = max(cu_q[s + 1] - cu_q[s], 0);
     const int nr = Lq > 0 && Lq <= kResidueMaxQ ? (Lq + P_res - 1) / P_res : 0;
     const int nq = Lq > kResidueMaxQ ? (Lq + P_pre - 1) / P_pre : 0;
     const int ir = wave_inclusive_sum(nr, lane);
@@ -840,8 +873,9 @@ VarlenShape varlen_shape(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q
   return v;
 }
 
-int launch_plan(const int32_t* cu_q, int32_t num_seqs, const VarlenShape& v, void* workspace, hipStream_t s) {
-  hipLaunchKernelGGL(varlen_plan, dim3(1), dim3(kPlanThreads), 0, s, cu_q, num_seqs, v.P, prefill_positions(v.g),
+int launch_plan(const int32_t* cu_q, const int32_t* cu_k, int32_t num_seqs, const VarlenShape& v, void* workspace,
+                hipStream_t s) {
+  hipLaunchKernelGGL(varlen_plan, dim3(1), dim3(kPlanThreads), 0, s, cu_q, cu_k, num_seqs, v.P, prefill_positions(v.g),
                      (int32_t*)((uint8_t*)workspace + v.lay.work), (int32_t*)((uint8_t*)workspace + v.lay.count),
                      (int32_t)v.items, (int32_t*)((uint8_t*)workspace + v.lay.work_pre),
                      (int32_t*)((uint8_t*)workspace + v.lay.count_pre), (int32_t)v.pre_items);
@@ -897,7 +931,7 @@ int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_str
   const bool partials = vs.partials;
   const Layout& lay = vs.lay;
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
-  if (pre_items + items > INT_MAX / 2) return fail(kUnsupported, "%s: too many prefill blocks", who);
+  if ((pre_items + items) * num_kv_heads > INT_MAX / 2) return fail(kUnsupported, "%s: too many prefill blocks", who);
   if (!workspace || workspace_bytes < lay.total)
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
@@ -935,7 +969,7 @@ int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_str
   int32_t* count_pre = (int32_t*)((uint8_t*)workspace + lay.count_pre);
 
   hipStream_t s = (hipStream_t)stream;
-  if (!planned && (rc = launch_plan(cu_seqlens_q, num_seqs, vs, workspace, s))) return rc;
+  if (!planned && (rc = launch_plan(cu_seqlens_q, cu_seqlens_k, num_seqs, vs, workspace, s))) return rc;
   if (pre_items > 0) {
     PrefillArgs a{};
     a.q = (const uint16_t*)q;
@@ -947,6 +981,9 @@ int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_str
     a.block_tables = paged ? block_tables : nullptr;
     a.table_width = table_width;
     a.block_size = paged ? block_size : 1;
+    a.tile_shift = -1;
+    if (paged && ((block_size / kTile) & (block_size / kTile - 1)) == 0)
+      a.tile_shift = __builtin_ctz((unsigned)(block_size / kTile));
     a.num_blocks = num_blocks;
     a.cu_q = cu_seqlens_q;
     a.cu_k = cu_seqlens_k;
@@ -961,8 +998,11 @@ int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_str
     a.scale_log2 = scale * kLog2e;
     a.out = (uint16_t*)out;
     a.out_stride = out_token_stride;
-    // One launch for both lists; its residue items always merge in LDS (no partials, no combine).
-    const dim3 mgrid((unsigned)(pre_items + items), num_kv_heads);
+    // One launch for both lists; its residue items always merge in LDS (no partials, no combine). The KV
+    // head varies fastest along the 1-D grid, so the work lists' order (longest first) is the dispatch order
+    // across all heads; and as dispatch goes round-robin over the 8 XCDs, with 8 KV heads the q-blocks of
+    // one head, which read the same K / V tiles, all run on one XCD and share its L2.
+    const dim3 mgrid((unsigned)((pre_items + items) * num_kv_heads));
     if (paged)
       hipLaunchKernelGGL(mixed_fwd<true>, mgrid, dim3(kResidues * kWave), 0, s, p, a);
     else
@@ -1011,18 +1051,18 @@ extern "C" int sd_varlen_attention_planned(const void* q, int64_t q_token_stride
                     out_token_stride, workspace, workspace_bytes, stream);
 }
 
-extern "C" int sd_varlen_plan(const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q,
-                              int32_t num_heads, int32_t num_kv_heads, void* workspace, size_t workspace_bytes,
-                              void* stream) {
+extern "C" int sd_varlen_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                              int32_t total_q, int32_t max_seqlen_q, int32_t num_heads, int32_t num_kv_heads,
+                              void* workspace, size_t workspace_bytes, void* stream) {
   const char* who = "sd_varlen_plan";
   if (num_seqs < 0 || total_q < 0 || max_seqlen_q < 0 || num_kv_heads <= 0 || num_heads <= 0 ||
       num_heads % num_kv_heads)
     return fail(kBadArgument, "%s: bad sizes", who);
   if (num_seqs == 0 || total_q == 0) return kOk;
-  if (!cu_seqlens_q) return fail(kBadArgument, "%s: null pointer", who);
+  if (!cu_seqlens_q || !cu_seqlens_k) return fail(kBadArgument, "%s: null pointer", who);
   const VarlenShape vs = varlen_shape(num_seqs, total_q, max_seqlen_q, num_heads, num_kv_heads);
   if (vs.items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)vs.items);
   if (!workspace || workspace_bytes < vs.lay.total)
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, vs.lay.total);
-  return launch_plan(cu_seqlens_q, num_seqs, vs, workspace, (hipStream_t)stream);
+  return launch_plan(cu_seqlens_q, cu_seqlens_k, num_seqs, vs, workspace, (hipStream_t)stream);
 }

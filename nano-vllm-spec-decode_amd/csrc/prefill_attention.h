@@ -44,6 +44,7 @@ struct PrefillArgs {
   const int32_t* block_tables;  // null: keys are rows cu_k[s] + j of k / v
   int32_t table_width;
   int32_t block_size;
+  int32_t tile_shift;           // log2(block_size / 32) when that is a power of two, else -1
   int64_t num_blocks;
   const int32_t* cu_q;
   const int32_t* cu_k;
@@ -75,7 +76,7 @@ constexpr int kStages = 2;                             // LDS stage buffers
 constexpr int kMaxBlocks = 1024;                       // block-table entries staged in LDS
 constexpr float kLazyLog2 = 8.f;                       // rescale threshold (exp2 domain)
 constexpr int kLoadsPerWave = kStageBytes / (kWaves * kWave * 16);  // 16-byte loads per lane per stage
-constexpr int kLdsBytes = kStages * kStageBytes + kMaxBlocks * 4;
+constexpr int kLdsBytes = kStages * kStageBytes + kMaxBlocks * 4 + kWaves * 4;  // + per-wave flags
 static_assert(kLoadsPerWave == 4, "stage loads: 8 waves x 4 x 1 KB");
 static_assert(kRowGroups * 32 == kPrefillRows, "q-block rows");
 // The parity merge reuses the stage buffers and the block ids: O of the four parity-1 waves (64 fp32 per
@@ -156,30 +157,42 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
     for (int s = 0; s < 8; ++s) qv[s] = bf16x8{};
   }
   wait_vm_all();  // Q and block ids in registers before any stage load is issued
+  bool bad = false;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int b = tid + i * kThreads;
-    if (b < nb_used) blk_ids[b] = blk_pre[i];
+    if (b < nb_used) {
+      blk_ids[b] = blk_pre[i];
+      bad |= blk_pre[i] < 0 || blk_pre[i] >= p.num_blocks;
+    }
   }
   static_assert(2 * kThreads >= kMaxBlocks, "two block ids per thread");
+  int32_t* bad_flags = blk_ids + kMaxBlocks;  // one per wave: the wave staged an invalid block id
+  const int wave_bad = __any(bad);
+  if (lane == 0) bad_flags[wave] = wave_bad;
   // The wave's rows span positions first..last: limits grow with the position.
   const int first_row = rg * 32, last_row = min(rg * 32 + 31, rows - 1);
   const bool wave_active = first_row < rows;
   const int lim_lo = wave_active ? min(max(Lk - Lq + p0 + first_row / p.g + 1, 0), kmax) : 0;
   const int lim_hi = wave_active ? min(max(Lk - Lq + p0 + last_row / p.g + 1, 0), kmax) : 0;
 
-  block_sync();  // block ids visible
+  block_sync();  // block ids and flags visible
+  // With valid ids only (the normal case) the tiles need no per-step check.
+  int any_bad = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) any_bad |= bad_flags[w];
+  any_bad = __builtin_amdgcn_readfirstlane(any_bad);
 
   // ---- stage loads: tiles 2*it and 2*it+1, K and V each, 1 KB per wave instruction ----
   const int64_t ksb = p.k_stride * 2, vsb = p.v_stride * 2;  // bytes per key row
-  auto tile_block = [&](int t, bool& ok) {  // block id of tile t (paged), block 0 when invalid
-    ok = true;
-    if (!kPaged || t >= ntiles) return 0;
-    const int bi = t * kTile / p.block_size;
-    const int blk = __builtin_amdgcn_readfirstlane(blk_ids[bi]);
-    ok = blk >= 0 && blk < p.num_blocks;
-    return ok ? blk : 0;
+  // Block-table index and in-block key offset of tile t (a tile never straddles two blocks).
+  auto tile_index = [&](int t) { return p.tile_shift >= 0 ? t >> p.tile_shift : t * kTile / p.block_size; };
+  auto tile_offset = [&](int t) {
+    return p.tile_shift >= 0 ? (t & ((1 << p.tile_shift) - 1)) * kTile : (t * kTile) % p.block_size;
   };
+  // The block id of tile t as read from LDS (0 past the last tile); read a step before it is needed, so
+  // that the read completes under that step's compute.
+  auto tile_block_raw = [&](int t) { return (!kPaged || t >= ntiles) ? 0 : blk_ids[tile_index(t)]; };
   // Wave w loads the tile of parity w / 4, K (w / 2 even) or V, 1 KB slots 4*(w%2) .. +3 of it: lane L of
   // slot j writes LDS bytes 16L.. of the slot, i.e. key 4j + L/16, physical chunk L%16, so it fetches the
   // logical chunk that the swizzle stores there. Stages past the last tile load valid rows that are never
@@ -189,7 +202,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   const int ld_slot0 = 4 * (wave % 2);
   const uint8_t* ld_src = (const uint8_t*)(ld_v ? p.v : p.k) + h * kD * 2;
   const int64_t ld_stride = ld_v ? vsb : ksb;
-  uint32_t ld_off[kLoadsPerWave];  // byte offset of this lane's chunk inside key row `key`
+  uint32_t ld_off[kLoadsPerWave];   // byte offset of this lane's chunk inside key row `key`
+  uint32_t ld_lane[kLoadsPerWave];  // paged: byte offset of that chunk from the tile's first key row
   int ld_key[kLoadsPerWave];
 #pragma unroll
   for (int i = 0; i < kLoadsPerWave; ++i) {
@@ -197,21 +211,27 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
     const int pc = lane % 16;
     ld_key[i] = key;
     ld_off[i] = 16 * (ld_v ? (pc ^ (4 * (key % 4))) : (pc ^ (key % 16)));
+    ld_lane[i] = (uint32_t)(key * ld_stride) + ld_off[i];
   }
-  auto load_stage = [&](int it, u32x4 (&r)[kLoadsPerWave]) {
+  // Paged: a wave-uniform base address (the tile's first key row) plus 32-bit lane offsets.
+  auto load_stage = [&](int it, int blk_raw, u32x4 (&r)[kLoadsPerWave]) {
     const int t = kParities * it + ld_par;
-    int64_t row0 = 0;  // cache slot of the tile's first key (paged)
     if (kPaged) {
-      bool ok;
-      const int blk = tile_block(t, ok);
-      if (t < ntiles && ok) row0 = (int64_t)blk * p.block_size + (t * kTile) % p.block_size;
-    }
+      const int blk = __builtin_amdgcn_readfirstlane(blk_raw);
+      int64_t row0 = 0;  // cache slot of the tile's first key; block 0 past the end or for an invalid id
+      if (t < ntiles && blk >= 0 && blk < p.num_blocks) row0 = (int64_t)blk * p.block_size + tile_offset(t);
+      const uint8_t* base = ld_src + row0 * ld_stride;
 #pragma unroll
-    for (int i = 0; i < kLoadsPerWave; ++i) {
-      const int64_t krow = kPaged ? row0 + ld_key[i] : (int64_t)k0 + min(t * kTile + ld_key[i], max(Lk - 1, 0));
-      r[i] = *(const u32x4*)(ld_src + krow * ld_stride + ld_off[i]);
+      for (int i = 0; i < kLoadsPerWave; ++i) r[i] = *(const u32x4*)(base + ld_lane[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kLoadsPerWave; ++i) {
+        const int64_t krow = (int64_t)k0 + min(t * kTile + ld_key[i], max(Lk - 1, 0));
+        r[i] = *(const u32x4*)(ld_src + krow * ld_stride + ld_off[i]);
+      }
     }
   };
+  auto stage_block = [&](int it) { return tile_block_raw(kParities * it + ld_par); };
   auto store_stage = [&](int it, const u32x4 (&r)[kLoadsPerWave]) {
     uint8_t* dst = lds + (it % kStages) * kStageBytes + ld_par * 2 * kTileBytes + (ld_v ? kTileBytes : 0) +
                    ld_slot0 * 1024 + lane * 16;
@@ -320,8 +340,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   // ---- pipeline: stage it in LDS, it+1 and it+2 in registers (ra / rb alternate) ----
   auto step = [&](int it) {
     const int t = kParities * it + par;
-    bool ok;
-    tile_block(t, ok);
+    bool ok = true;
+    if (kPaged && any_bad && t < ntiles) {
+      const int blk = __builtin_amdgcn_readfirstlane(blk_ids[tile_index(t)]);
+      ok = blk >= 0 && blk < p.num_blocks;
+    }
     if (wave_active && t < ntiles && ok && t * kTile < lim_hi) {
       const uint8_t* kt = lds + (it % kStages) * kStageBytes + par * 2 * kTileBytes;
       compute(kt, kt + kTileBytes, t, t * kTile + kTile > lim_lo);
@@ -329,23 +352,25 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   };
   u32x4 ra[kLoadsPerWave], rb[kLoadsPerWave];
   if (niter > 0) {
-    load_stage(0, ra);
-    load_stage(1, rb);
+    load_stage(0, stage_block(0), ra);
+    load_stage(1, stage_block(1), rb);
     store_stage(0, ra);
-    load_stage(2, ra);
+    load_stage(2, stage_block(2), ra);
     block_sync();  // stage 0 in LDS
   }
   // Straight-line halves (no conditional loads or stores) so that every wait count is static: stages
   // past the end are stored into a buffer that is never read again, and an odd last half-step computes
   // nothing (its tile index is >= ntiles).
   for (int it = 0; it < niter; it += 2) {
+    const int blk3 = stage_block(it + 3);
     step(it);
     store_stage(it + 1, rb);  // buffer (it+1)%2 was last read in iteration it-1
-    load_stage(it + 3, rb);
+    load_stage(it + 3, blk3, rb);
     block_sync();
+    const int blk4 = stage_block(it + 4);
     step(it + 1);
     store_stage(it + 2, ra);
-    load_stage(it + 4, ra);
+    load_stage(it + 4, blk4, ra);
     block_sync();
   }
 

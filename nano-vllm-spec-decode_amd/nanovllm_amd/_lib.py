@@ -30,7 +30,7 @@ SIGNATURES = {
     "sd_varlen_attention": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p,
                                    _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                    _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
-    "sd_varlen_plan": (_i32, [_c_void_p, _i32, _i32, _i32, _i32, _i32, _c_void_p, _size, _c_void_p]),
+    "sd_varlen_plan": (_i32, [_c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _c_void_p, _size, _c_void_p]),
     "sd_varlen_attention_planned": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i32,
                                            _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
                                            _i32, _f32, _c_void_p, _i64, _c_void_p, _size, _c_void_p]),

@@ -85,8 +85,8 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     """flash_attn_varlen_func(causal=True) semantics (attention.py:64-70). q [Nq, Hq, D]; k / v are fresh
     [Nk, Hkv, D] rows, or the paged caches [NB, bs, Hkv, D] when block_table is given.
 
-    plan_owner: an object that lives exactly as long as this cu_seqlens_q (the step's Context). The work
-    lists derived from cu_seqlens_q are then computed once and reused by every later call with the same
+    plan_owner: an object that lives exactly as long as this cu_seqlens_q / cu_seqlens_k (the step's Context).
+    The work lists derived from them are then computed once and reused by every later call with the same
     owner and sizes, as long as no other plan has replaced them in the varlen workspace. Never reused while
     a graph is being captured."""
     global _plan_in_workspace
@@ -116,12 +116,13 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     stream = _lib.stream_of(q.device)
     fn = lib.sd_varlen_attention
     if plan_owner is not None and not torch.cuda.is_current_stream_capturing():
-        key = (id(plan_owner), cu_seqlens_q.data_ptr(), nseq, Nq, max_seqlen_q, Hq, Hkv, ws.data_ptr(), ws.numel())
+        key = (id(plan_owner), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq, max_seqlen_q, Hq, Hkv,
+               ws.data_ptr(), ws.numel())
         if getattr(plan_owner, "_sd_varlen_plan", None) == key and _plan_in_workspace == key:
             plan_stats["reuses"] += 1
         else:
-            _lib.check(lib.sd_varlen_plan(cu_seqlens_q.data_ptr(), nseq, Nq, max_seqlen_q, Hq, Hkv, ws.data_ptr(),
-                                          ws.numel(), stream), "sd_varlen_plan")
+            _lib.check(lib.sd_varlen_plan(cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq, max_seqlen_q,
+                                          Hq, Hkv, ws.data_ptr(), ws.numel(), stream), "sd_varlen_plan")
             plan_owner._sd_varlen_plan = key
             _plan_in_workspace = key
             plan_stats["plans"] += 1
