@@ -10,7 +10,7 @@ profiles/), null if that summary is absent.
 
 Also reported (same JSON line): the KV-cache scatter (2048 rows, 10% padding slots), the rejection sampler
 (S 64, K 4, V 151936, T 0 and T 1 with draft logits) and a 2048-token mixed prefill+decode attention step
-over 36 layers (tok/s), plus a CPU baseline: the oracle (PyTorch CPU restatement) timed on the headline
+over 36 layers replayed as one HIP graph by the mixed-step runtime (tok/s), plus a CPU baseline: the oracle (PyTorch CPU restatement) timed on the headline
 workload for about 10 s on 16 host threads.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10]
@@ -141,48 +141,59 @@ def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
 
 
 def bench_mixed_attention(dev, steps, warmup, layers=36):
-    """Attention phase of a 2048-token-budget mixed step: per layer, store this step's KV then varlen paged
-    attention over 48 decode sequences (k = 4) and 3 prefill chunks (config-5 lengths)."""
+    """Attention phase of a 2048-token-budget mixed step (48 verify requests with k = 4 and 3 prefill chunks,
+    config-5 lengths, Qwen3-8B shapes): per layer, store this step's KV then varlen paged attention, for 36
+    layers. Timed as one HIP-graph replay per step through the mixed-step runtime (plan + 36 x (store +
+    attention), metadata refreshed by one host-to-device copy per step), and as eager per-layer calls."""
     import numpy as np
     import torch
+    from types import SimpleNamespace
     from attn_cases import paged_cache, queries
+    from nanovllm_amd.engine.mixed_step import MixedStepRunner
     from nanovllm_amd.layers.attention import store_kvcache, varlen_attention
+    from test_gpu_mixed_step import K, _requests
     from test_gpu_varlen import mixed_step
     lq, lk = mixed_step(0)
+    nd = 48
     W = math.ceil(max(lk) / BLOCK)
     kc, vc, tables = paged_cache(dev, lk, HKV, D, W=W, seed=5)
     caches = [(kc, vc)] + [(torch.empty_like(kc).copy_(kc), torch.empty_like(vc).copy_(vc)) for _ in range(layers - 1)]
-    Nq = sum(lq)
-    q = queries(dev, Nq, HQ, D, seed=6)
-    knew = queries(dev, Nq, HKV, D, seed=7)
-    vnew = queries(dev, Nq, HKV, D, seed=8)
-    tb = tables.cpu()
-    slots = []
-    for s, (a, b) in enumerate(zip(lq, lk)):
-        slots += [int(tb[s, p // BLOCK]) * BLOCK + p % BLOCK for p in range(b - a, b)]
-    slots = torch.tensor(slots, dtype=torch.int32, device=dev)
-    cu_q = torch.tensor([0] + np.cumsum(lq).tolist(), dtype=torch.int32, device=dev)
-    cu_k = torch.tensor([0] + np.cumsum(lk).tolist(), dtype=torch.int32, device=dev)
+    runner = MixedStepRunner([SimpleNamespace(k_cache=a, v_cache=b) for a, b in caches], HQ, HKV, D, D ** -0.5,
+                             block_size=BLOCK, max_num_batched_tokens=2048, max_num_seqs=64, table_width=W)
+    layout = runner.prepare(_requests(lq, lk, tables.cpu(), nd), K)
+    Nq, N = layout["n"], layout["N"]
+    runner.bufs["q"][:N] = queries(dev, N, HQ, D, seed=6)
+    runner.bufs["k"][:N] = queries(dev, N, HKV, D, seed=7)
+    runner.bufs["v"][:N] = queries(dev, N, HKV, D, seed=8)
+    wall, ev = timed(lambda: runner.run(layout), steps, warmup)
+    t = sum(ev) / len(ev)
+
+    # eager: the same step as 36 x (store_kvcache + varlen_attention) Python calls (plan reused per step)
+    q, knew, vnew = runner.bufs["q"][:Nq], runner.bufs["k"][:Nq], runner.bufs["v"][:Nq]
+    slots = torch.tensor(layout["slot_mapping"], dtype=torch.int32, device=dev)
+    cu_q = torch.tensor(layout["cu_seqlens_q"], dtype=torch.int32, device=dev)
+    cu_k = torch.tensor(layout["cu_seqlens_k"], dtype=torch.int32, device=dev)
     out = torch.empty(Nq, HQ, D, dtype=torch.bfloat16, device=dev)
 
-    def step():
-        owner = types.SimpleNamespace()  # the step's context: layer 1 plans the work lists, the others reuse them
+    def eager_step():
+        owner = SimpleNamespace()  # the step's context: layer 1 plans the work lists, the others reuse them
         for kcl, vcl in caches:
             store_kvcache(knew, vnew, kcl, vcl, slots)
-            varlen_attention(q, kcl, vcl, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables, out=out,
-                             plan_owner=owner)
+            varlen_attention(q, kcl, vcl, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables, out=out, plan_owner=owner)
 
-    wall, ev = timed(step, steps, warmup)
-    t = sum(ev) / len(ev)
-    nd = 48
+    _, eager_ev = timed(eager_step, steps, warmup)
+    t_eager = sum(eager_ev) / len(eager_ev)
     flops = sum(4 * HQ * D * (a * (b - a) + a * (a + 1) / 2) for a, b in zip(lq[nd:], lk[nd:]))
     dec_bytes = decode_bytes(lk[:nd], 5)
-    # One layer's attention kernel (work lists planned beforehand), whole step and its prefill chunks alone.
-    layer_s = planned_varlen_time(q, kc, vc, lq, lk, tables)
+    # One layer's attention kernel (work lists planned beforehand), whole step and its prefill chunks alone,
+    # each call on the next layer's caches.
+    layer_s = planned_varlen_time(q, caches, lq, lk, tables)
     pre = slice(sum(lq[:nd]), Nq)
-    prefill_s = planned_varlen_time(q[pre], kc, vc, lq[nd:], lk[nd:], tables[nd:].contiguous())
-    return dict(ms=t * 1e3, tok_s=Nq / t, query_tokens=Nq, decode_seqs=nd, prefill_chunks=len(lq) - nd,
-                prefill_flops_per_layer=flops, decode_bytes_per_layer=dec_bytes,
+    prefill_s = planned_varlen_time(q[pre], caches, lq[nd:], lk[nd:], tables[nd:].contiguous())
+    return dict(ms=round(t * 1e3, 4), tok_s=round(Nq / t, 1), timing="one HIP-graph replay per step",
+                eager_ms=round(t_eager * 1e3, 4), eager_tok_s=round(Nq / t_eager, 1),
+                query_tokens=Nq, bucket_tokens=N, bucket_seqs=layout["S"], decode_seqs=nd,
+                prefill_chunks=len(lq) - nd, prefill_flops_per_layer=flops, decode_bytes_per_layer=dec_bytes,
                 layer_attention_us=round(layer_s * 1e6, 2),
                 prefill_only_us=round(prefill_s * 1e6, 2),
                 prefill_only_tflops=round(flops / prefill_s / 1e12, 1),
@@ -190,9 +201,11 @@ def bench_mixed_attention(dev, steps, warmup, layers=36):
                 layer_prefill_mfma_frac=round(flops / layer_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4))
 
 
-def planned_varlen_time(q, kc, vc, lq, lk, tables):
+def planned_varlen_time(q, caches, lq, lk, tables):
     """Seconds per sd_varlen_attention_planned call (the attention kernel alone; the work lists are planned
-    once outside the timed graph, as the per-layer loop of a step does)."""
+    once outside the timed graph, as the per-layer loop of a step does). The calls cycle through `caches`
+    (one (k, v) pair per layer), so that a layer's KV is not still in the 256 MB last-level cache from the
+    call before, as in a real step."""
     import numpy as np
     import torch
     from nanovllm_amd import _lib
@@ -208,14 +221,17 @@ def planned_varlen_time(q, kc, vc, lq, lk, tables):
     stream = lambda: torch.cuda.current_stream().cuda_stream
     _lib.check(lib.sd_varlen_plan(cu_q.data_ptr(), cu_k.data_ptr(), nseq, Nq, max(lq), HQ, HKV, ws.data_ptr(), nbytes,
                                   stream()), "sd_varlen_plan")
+    turn = [0]
 
     def call():
+        kc, vc = caches[turn[0] % len(caches)]
+        turn[0] += 1
         _lib.check(lib.sd_varlen_attention_planned(
             qr.data_ptr(), qr.stride(0), kc.data_ptr(), HKV * D, vc.data_ptr(), HKV * D, 0, kc.size(0), BLOCK,
             tables.data_ptr(), tables.size(1), cu_q.data_ptr(), cu_k.data_ptr(), nseq, Nq, max(lq), max(lk), HQ,
             HKV, D, D ** -0.5, out.data_ptr(), out.stride(0), ws.data_ptr(), nbytes, stream()),
             "sd_varlen_attention_planned")
-    return graph_timed(call)
+    return graph_timed(call, reps=len(caches))
 
 
 def cpu_baseline(inputs, min_seconds=10.0, max_reps=8):
