@@ -73,7 +73,8 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     return out
 
 
-# Key of the varlen plan held by the varlen workspace (set by the last sd_varlen_plan call).
+# (owner, key) of the varlen plan held by the varlen workspace (set by the last sd_varlen_plan call). The
+# owner is held here (not tagged: the Context dataclass has slots), so its id cannot be reused meanwhile.
 _plan_in_workspace = None
 plan_stats = {"plans": 0, "reuses": 0}
 
@@ -116,15 +117,14 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     stream = _lib.stream_of(q.device)
     fn = lib.sd_varlen_attention
     if plan_owner is not None and not torch.cuda.is_current_stream_capturing():
-        key = (id(plan_owner), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq, max_seqlen_q, Hq, Hkv,
-               ws.data_ptr(), ws.numel())
-        if getattr(plan_owner, "_sd_varlen_plan", None) == key and _plan_in_workspace == key:
+        key = (cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq, max_seqlen_q, Hq, Hkv, ws.data_ptr(),
+               ws.numel())
+        if _plan_in_workspace is not None and _plan_in_workspace[0] is plan_owner and _plan_in_workspace[1] == key:
             plan_stats["reuses"] += 1
         else:
             _lib.check(lib.sd_varlen_plan(cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq, max_seqlen_q,
                                           Hq, Hkv, ws.data_ptr(), ws.numel(), stream), "sd_varlen_plan")
-            plan_owner._sd_varlen_plan = key
-            _plan_in_workspace = key
+            _plan_in_workspace = (plan_owner, key)
             plan_stats["plans"] += 1
         fn = lib.sd_varlen_attention_planned
     else:

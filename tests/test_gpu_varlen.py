@@ -146,8 +146,8 @@ def test_plan_reuse_across_layers(device):
     """The step's work lists are planned once per owner (the step's Context) and reused by later layers:
     bitwise equal to unplanned calls; a different owner replans, and so does the first owner afterwards
     because its plan was replaced in the workspace."""
-    import types
     from nanovllm_amd.layers import attention as att
+    from nanovllm_amd.utils.context import Context
     Hq, Hkv, D = 32, 8, 128
     lq, lk = mixed_step(3)
     kc, vc, tables = paged_cache(device, lk, Hkv, D, W=math.ceil(max(lk) / BLOCK), seed=14)
@@ -155,7 +155,7 @@ def test_plan_reuse_across_layers(device):
     cu_q, cu_k = _cu(lq, device), _cu(lk, device)
     args = (q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
     ref = varlen_attention(*args)
-    owner = types.SimpleNamespace()
+    owner = Context(True, cu_q, cu_k, max(lq), max(lk))   # the step's Context (a slotted dataclass)
     plans0, reuses0 = att.plan_stats["plans"], att.plan_stats["reuses"]
     for _ in range(3):
         assert torch.equal(varlen_attention(*args, plan_owner=owner), ref)
@@ -163,7 +163,7 @@ def test_plan_reuse_across_layers(device):
     lq2, lk2 = [5] * 8 + [40], [300] * 8 + [90]
     kc2, vc2, tb2 = paged_cache(device, lk2, Hkv, D, seed=16)
     q2 = queries(device, sum(lq2), Hq, D, seed=17)
-    other = types.SimpleNamespace()
+    other = Context(True)
     out2 = varlen_attention(q2, kc2, vc2, _cu(lq2, device), _cu(lk2, device), max(lq2), max(lk2), D ** -0.5, tb2,
                             plan_owner=other)
     assert torch.equal(out2, varlen_attention(q2, kc2, vc2, _cu(lq2, device), _cu(lk2, device), max(lq2),
