@@ -201,6 +201,23 @@ def bench_mixed_attention(dev, steps, warmup, layers=36):
                 layer_prefill_mfma_frac=round(flops / layer_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4))
 
 
+def bench_prefill(dev):
+    """The prefill q-block kernel on its own at sizes that fill the GPU (Qwen3-8B shapes, paged KV): 16
+    chunks of 1024 queries after a 1024-token cached prefix, and one fresh 2048-token prompt. FLOPs are the
+    causal attention's 4*Hq*D*(Lq*P + Lq(Lq+1)/2) per chunk."""
+    from attn_cases import paged_cache, queries
+    res = {}
+    for name, lq, lk in (("16x1024_after_1024", [1024] * 16, [2048] * 16), ("1x2048", [2048], [2048])):
+        kc, vc, tables = paged_cache(dev, lk, HKV, D, W=math.ceil(max(lk) / BLOCK), seed=21)
+        q = queries(dev, sum(lq), HQ, D, seed=22)
+        t = planned_varlen_time(q, [(kc, vc)], lq, lk, tables)
+        flops = sum(4 * HQ * D * (a * (b - a) + a * (a + 1) / 2) for a, b in zip(lq, lk))
+        res[name] = dict(us=round(t * 1e6, 2), tflops=round(flops / t / 1e12, 1),
+                         mfma_frac=round(flops / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4))
+        del kc, vc, tables, q
+    return res
+
+
 def planned_varlen_time(q, caches, lq, lk, tables):
     """Seconds per sd_varlen_attention_planned call (the attention kernel alone; the work lists are planned
     once outside the timed graph, as the per-layer loop of a step does). The calls cycle through `caches`
@@ -323,6 +340,7 @@ def main():
         result["verify_sampler"] = bench_sampler(dev, max(10, args.steps // 2), args.warmup)
         mixed = bench_mixed_attention(dev, max(5, args.steps // 10), 2)
         result["mixed_step_attention"] = mixed
+        result["prefill_kernel"] = bench_prefill(dev)
     if not args.skip_extras and not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(head["inputs"])
     print(json.dumps(result), flush=True)
