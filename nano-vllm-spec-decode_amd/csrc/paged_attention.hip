@@ -490,9 +490,15 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
 }
 
 // A varlen call with long query runs: one launch for both work lists, so that the prefill q-blocks (MFMA
-// and latency bound) and the decode / verify items (HBM bound) share the CUs. x < a.max_items: prefill
-// q-block x; otherwise residue item x - a.max_items with all eight residues in the workgroup (merged in
-// LDS, two row tiles).
+// and latency bound) and the decode / verify items (HBM bound) share the CUs. Slot x of the dispatch order
+// takes the lists interleaved, two prefill q-blocks then one residue item (each list in its own order,
+// longest first), then the rest of the longer list: the long prefill blocks start early without holding
+// every CU while the decode rows wait, so HBM keeps streaming under the prefill math (config-5 layer 59 ->
+// 49 us against the prefill list first). A residue item runs all eight residues in the workgroup (merged in
+// LDS, two row tiles). Slots past both lists exit; the grid has kMixedSlack spare slots for a partial last
+// group.
+constexpr int kMixedPre = 2, kMixedRes = 1;
+constexpr int kMixedSlack = kMixedPre + kMixedRes - 2;
 constexpr int kMixedLds = lds_bytes(kResidues) > prefill::kLdsBytes ? lds_bytes(kResidues) : prefill::kLdsBytes;
 static_assert(prefill::kThreads == kResidues * kWave, "both halves use 512-thread workgroups");
 
@@ -501,10 +507,25 @@ __global__ __launch_bounds__(kResidues * kWave, 2) void mixed_fwd(Params p, Pref
   __shared__ __attribute__((aligned(16))) uint8_t lds[kMixedLds];
   const int h = blockIdx.x % a.Hkv;
   const int x = blockIdx.x / a.Hkv;
-  if (x < a.max_items)
-    prefill::prefill_body<kPaged>(a, lds, x, h);
-  else
-    attn_body<2, true, kPaged, kResidues, 1>(p, lds, x - a.max_items, h, 0);
+  const int np = *a.work_count, nr = *p.work_count;  // the plan's counts (each at most its grid share)
+  constexpr int G = kMixedPre + kMixedRes;
+  const int groups = min((np + kMixedPre - 1) / kMixedPre, (nr + kMixedRes - 1) / kMixedRes);
+  int pre = -1, res = -1;
+  if (x < groups * G) {
+    const int j = x / G, s = x % G;
+    if (s < kMixedPre)
+      pre = j * kMixedPre + s;
+    else
+      res = j * kMixedRes + s - kMixedPre;
+  } else if (groups * kMixedPre < np) {
+    pre = groups * kMixedPre + x - groups * G;
+  } else {
+    res = groups * kMixedRes + x - groups * G;
+  }
+  if (pre >= 0 && pre < np)
+    prefill::prefill_body<kPaged>(a, lds, pre, h);
+  else if (res >= 0 && res < nr)
+    attn_body<2, true, kPaged, kResidues, 1>(p, lds, res, h, 0);
 }
 
 // Merges the eight residue partials of every row, in residue order, with the same fma chain as the
@@ -931,7 +952,8 @@ int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_str
   const bool partials = vs.partials;
   const Layout& lay = vs.lay;
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
-  if ((pre_items + items) * num_kv_heads > INT_MAX / 2) return fail(kUnsupported, "%s: too many prefill blocks", who);
+  if ((pre_items + items + kMixedSlack) * num_kv_heads > INT_MAX / 2)
+    return fail(kUnsupported, "%s: too many prefill blocks", who);
   if (!workspace || workspace_bytes < lay.total)
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
@@ -1002,7 +1024,7 @@ int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_str
     // head varies fastest along the 1-D grid, so the work lists' order (longest first) is the dispatch order
     // across all heads; and as dispatch goes round-robin over the 8 XCDs, with 8 KV heads the q-blocks of
     // one head, which read the same K / V tiles, all run on one XCD and share its L2.
-    const dim3 mgrid((unsigned)((pre_items + items) * num_kv_heads));
+    const dim3 mgrid((unsigned)((pre_items + items + kMixedSlack) * num_kv_heads));
     if (paged)
       hipLaunchKernelGGL(mixed_fwd<true>, mgrid, dim3(kResidues * kWave), 0, s, p, a);
     else
