@@ -1,7 +1,7 @@
 // Speculative-decoding verifier and token sampler over the full vocabulary (replaces verify_drafts and
 // Sampler.forward, nanovllm/layers/sampler.py:5-103).
 //
-// Three kernels, two of them HBM-streaming over [rows, vocab] tables. A row is cut into at most
+// Four kernels, two of them HBM-streaming over [rows, vocab] tables. A row is cut into at most
 // kSpans contiguous spans (a multiple of 4 entries each, none empty); a 256-thread workgroup streams one
 // span with 4-entry loads (16 B for fp32, 8 B for bf16; scalar loads when the rows are not aligned).
 //   1. row_stats      (row, span): first argmax of the raw logits of target rows; for rows with temperature
@@ -10,13 +10,17 @@
 //   2. verify_decide  (seq): merges span stats in span order (argmax, logsumexp), applies the accept rule
 //                     u * q(d) < p(d) (or top1 == d for greedy rows) to the leading run of real guesses,
 //                     writes num_accepted and, for greedy rows, next_token.
-//   3. verify_resample(seq, span): random rows only: the first argmax of p / max(E, 1e-10) and of
+//   3. verify_resample(seq, span): random rows only, over up to 64 spans per row (a single row per
+//                     sequence: more spans keep a small batch spread over the GPU): the first argmax of
+//                     p / max(E, 1e-10) and of
 //                     residual / max(E, 1e-10) with p = softmax(row a / T), residual = max(p - q, 0) (or p
-//                     with the rejected n-gram guess zeroed), and whether any residual is positive; the last
-//                     span workgroup of a sequence merges the span candidates in order and picks the token.
+//                     with the rejected n-gram guess zeroed), and whether any residual is positive.
+//   4. verify_finish  (seq): random rows only: merges the span candidates and picks the token.
 // Every reduction has a fixed order, so results are deterministic; ties resolve to the first index (and a
 // NaN counts as the largest value), as torch.argmax does.
 #include <math.h>
+
+#include <algorithm>
 
 #include "sd_common.h"
 #include "../../include/sd_attn.h"
@@ -76,6 +80,11 @@ __device__ __forceinline__ float4 load_logit4(const void* base, int64_t idx) {
                      __builtin_bit_cast(float, w.y << 16), __builtin_bit_cast(float, w.y & 0xffff0000u));
 }
 
+// exp(x) as one v_exp_f32 of x * log2(e): for the per-entry exponentials of the streaming kernels. Its
+// relative error (the rounding of the product, about |x| * 2^-24) stays near 1e-6 over the range softmax
+// sees; the few exponentials of the merges keep expf.
+__device__ __forceinline__ float exp_entry(float x) { return exp2_fast(x * 1.4426950408889634f); }
+
 // Online (max, sum of exp(x - max)) of one thread's entries; an infinite or empty max uses 0 as the shift.
 struct OnlineSum {
   float m = -INFINITY, s = 0.f;
@@ -85,10 +94,10 @@ struct OnlineSum {
     if (ml > m) {
       const float old = shift();
       m = ml;
-      s *= expf(old - shift());
+      s *= exp_entry(old - shift());
     }
     const float sh = shift();
-    s += expf(x0 - sh) + expf(x1 - sh) + expf(x2 - sh) + expf(x3 - sh);
+    s += exp_entry(x0 - sh) + exp_entry(x1 - sh) + exp_entry(x2 - sh) + exp_entry(x3 - sh);
   }
 };
 
@@ -175,13 +184,13 @@ struct VParams {
   int64_t draft_stride;
   const float* uniforms;          // [S, K]
   const float* noise;             // [S, V]
-  int32_t S, K, V, nchunk, span;  // nchunk spans of `span` entries (the last may be shorter)
+  int32_t S, K, V, nchunk, span;  // row_stats: nchunk spans of `span` entries (the last may be shorter)
+  int32_t rchunk, rspan;          // verify_resample: rchunk spans of `rspan` entries
   int64_t* out_a;
   int64_t* out_next;
   RowStat* stats;                 // [(S*(K+1) + S*K) rows][nchunk]
   SeqInfo* info;                  // [S]
-  Cand* cand;                     // [S][nchunk]
-  int32_t* done;                  // [S] finished resample workgroups
+  Cand* cand;                     // [S][rchunk]
 };
 
 template <int DT, int DDT, bool kVec>
@@ -216,19 +225,10 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
       bi = v;
     }
   };
-  for (int v = v0 + 4 * threadIdx.x; v < v1; v += 4 * kThreads) {
-    float r[4];
-    if (kVec && v + 4 <= v1) {
-      const float4 q4 = is_target ? load_logit4<DT>(base, v) : load_logit4<DDT>(base, v);
-      r[0] = q4.x;
-      r[1] = q4.y;
-      r[2] = q4.z;
-      r[3] = q4.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        r[e] = v + e < v1 ? (is_target ? load_logit<DT>(base, v + e) : load_logit<DDT>(base, v + e)) : -INFINITY;
-    }
+  auto load4 = [&](int v) {
+    return is_target ? load_logit4<DT>(base, v) : load_logit4<DDT>(base, v);
+  };
+  auto body = [&](int v, const float (&r)[4]) {  // entries v .. v+3 (those below v1)
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       if (v + e < v1) visit(r[e], v + e);
@@ -238,6 +238,37 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
       for (int e = 0; e < 4; ++e) x[e] = v + e < v1 ? (T == 1.f ? r[e] : r[e] / T) : -INFINITY;  // x / 1 == x
       os.add4(x[0], x[1], x[2], x[3]);
     }
+  };
+  // A thread visits v0 + 4*tid, then every 4*kThreads entries, in increasing order; the aligned main loop
+  // issues four of those loads before using any (the same visiting order, more loads in flight).
+  constexpr int kStep = 4 * kThreads;
+  int v = v0 + 4 * threadIdx.x;
+  if (kVec) {
+    for (; v + 3 * kStep + 4 <= v1; v += 4 * kStep) {
+      float4 q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) q[u] = load4(v + u * kStep);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float r[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+        body(v + u * kStep, r);
+      }
+    }
+  }
+  for (; v < v1; v += kStep) {
+    float r[4];
+    if (kVec && v + 4 <= v1) {
+      const float4 q4 = load4(v);
+      r[0] = q4.x;
+      r[1] = q4.y;
+      r[2] = q4.z;
+      r[3] = q4.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        r[e] = v + e < v1 ? (is_target ? load_logit<DT>(base, v + e) : load_logit<DDT>(base, v + e)) : -INFINITY;
+    }
+    body(v, r);
   }
   RowStat st;
   st.max_x = 0.f;
@@ -332,7 +363,6 @@ __global__ __launch_bounds__(64) void verify_decide(VParams p) {
   int a = 0;
   while (a < K && accj[a]) ++a;
   p.out_a[seq] = a;
-  p.done[seq] = 0;
   SeqInfo info{};
   info.a = a;
   info.random = random ? 1 : 0;
@@ -358,24 +388,36 @@ __global__ __launch_bounds__(64) void verify_decide(VParams p) {
   p.info[seq] = info;
 }
 
-__device__ void finish_seq(const VParams& p, int seq, const SeqInfo& info) {
-  const volatile Cand* c = p.cand + (int64_t)seq * p.nchunk;
-  float pv = c[0].p_val, rv = c[0].r_val;
-  int pi = c[0].p_idx, ri = c[0].r_idx;
-  int any_res = c[0].any_res;
-  for (int k = 1; k < p.nchunk; ++k) {
-    if (better(c[k].p_val, c[k].p_idx, pv, pi)) {
-      pv = c[k].p_val;
-      pi = c[k].p_idx;
+// One workgroup per random sequence: thread k reads span k's candidate (all reads in flight together),
+// then the same block reductions as inside a span. The argmax order (value, then lower index) makes the
+// result independent of the reduction tree. A kernel of its own: merging in the last span workgroup would
+// need device-scope fences (an L2 write-back and invalidate per workgroup on this GPU), which cost more
+// than the launch.
+__global__ __launch_bounds__(kThreads) void verify_finish(VParams p) {
+  __shared__ float shf[4];
+  __shared__ int shi[4];
+  const int seq = blockIdx.x;
+  const SeqInfo info = p.info[seq];
+  if (!info.random) return;
+  float pv = -INFINITY, rv = -INFINITY;
+  int pi = 0x7fffffff, ri = 0x7fffffff, any_res = 0;
+  for (int k = threadIdx.x; k < p.rchunk; k += kThreads) {
+    const Cand c = p.cand[(int64_t)seq * p.rchunk + k];
+    if (better(c.p_val, c.p_idx, pv, pi)) {
+      pv = c.p_val;
+      pi = c.p_idx;
     }
-    if (better(c[k].r_val, c[k].r_idx, rv, ri)) {
-      rv = c[k].r_val;
-      ri = c[k].r_idx;
+    if (better(c.r_val, c.r_idx, rv, ri)) {
+      rv = c.r_val;
+      ri = c.r_idx;
     }
-    any_res |= c[k].any_res;
+    any_res |= c.any_res;
   }
+  block_argmax(pv, pi, shf, shi);
+  block_argmax(rv, ri, shf, shi);
+  any_res = __syncthreads_or(any_res);
   const bool use_res = info.resid_mode == 2 && info.rejected && any_res;
-  p.out_next[seq] = use_res ? ri : pi;
+  if (threadIdx.x == 0) p.out_next[seq] = use_res ? ri : pi;
 }
 
 template <int DT, int DDT, bool kVec>
@@ -397,15 +439,61 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
     dbase = DDT == SD_DTYPE_F32 ? (const void*)((const float*)p.draft_logits + drow * p.draft_stride)
                                 : (const void*)((const uint16_t*)p.draft_logits + drow * p.draft_stride);
   const float* noise = p.noise ? p.noise + (int64_t)seq * p.V : nullptr;  // missing noise: E = 1
-  const int v0 = chunk * p.span;
-  const int v1 = min(v0 + p.span, p.V);
+  const int v0 = chunk * p.rspan;
+  const int v1 = min(v0 + p.rspan, p.V);
   float pv = -INFINITY, rv = -INFINITY;
   int pi = 0x7fffffff, ri = 0x7fffffff;
   int any_res = 0;
-  for (int v = v0 + 4 * threadIdx.x; v < v1; v += 4 * kThreads) {
-    const bool full = kVec && v + 4 <= v1;
-    float l[4], E[4], ld[4];
-    if (full) {
+  auto body = [&](int v, const float (&l)[4], const float (&E)[4], const float (&ld)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = v + e;
+      if (idx >= v1) continue;
+      float prob = exp_entry((T == 1.f ? l[e] : l[e] / T) - info.Ma) / info.Sa;  // divided, as softmax does
+      const float Ee = noise ? fmaxf(E[e], 1e-10f) : 1.f;
+      if (info.resid_mode == 1 && info.rejected && idx == info.guess) prob = 0.f;
+      const float sp = prob / Ee;
+      if (better(sp, idx, pv, pi)) {
+        pv = sp;
+        pi = idx;
+      }
+      if (dbase) {
+        const float q = exp_entry((T == 1.f ? ld[e] : ld[e] / T) - info.Md) / info.Sd;
+        const float res = fmaxf(prob - q, 0.f);
+        any_res |= res > 0.f;
+        const float sr = res / Ee;
+        if (better(sr, idx, rv, ri)) {
+          rv = sr;
+          ri = idx;
+        }
+      }
+    }
+  };
+  // Same per-thread visiting order as row_stats; the aligned main loop has the loads of two steps (target,
+  // noise and draft rows) in flight before using them.
+  constexpr int kStep = 4 * kThreads;
+  int v = v0 + 4 * threadIdx.x;
+  if (kVec) {
+    for (; v + kStep + 4 <= v1; v += 2 * kStep) {
+      float4 t4[2], e4[2], d4[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        t4[u] = load_logit4<DT>(tbase, v + u * kStep);
+        e4[u] = noise ? *(const float4*)(noise + v + u * kStep) : make_float4(1.f, 1.f, 1.f, 1.f);
+        d4[u] = dbase ? load_logit4<DDT>(dbase, v + u * kStep) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const float l[4] = {t4[u].x, t4[u].y, t4[u].z, t4[u].w};
+        const float E[4] = {e4[u].x, e4[u].y, e4[u].z, e4[u].w};
+        const float ld[4] = {d4[u].x, d4[u].y, d4[u].z, d4[u].w};
+        body(v + u * kStep, l, E, ld);
+      }
+    }
+  }
+  for (; v < v1; v += kStep) {
+    float l[4], E[4] = {1.f, 1.f, 1.f, 1.f}, ld[4] = {0.f, 0.f, 0.f, 0.f};
+    if (kVec && v + 4 <= v1) {
       const float4 t4 = load_logit4<DT>(tbase, v);
       l[0] = t4.x, l[1] = t4.y, l[2] = t4.z, l[3] = t4.w;
       if (noise) {
@@ -425,29 +513,7 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
         if (dbase) ld[e] = in ? load_logit<DDT>(dbase, v + e) : 0.f;
       }
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int idx = v + e;
-      if (idx >= v1) continue;
-      float prob = expf((T == 1.f ? l[e] : l[e] / T) - info.Ma) / info.Sa;  // divided, as softmax does
-      const float Ee = noise ? fmaxf(E[e], 1e-10f) : 1.f;
-      if (info.resid_mode == 1 && info.rejected && idx == info.guess) prob = 0.f;
-      const float sp = prob / Ee;
-      if (better(sp, idx, pv, pi)) {
-        pv = sp;
-        pi = idx;
-      }
-      if (dbase) {
-        const float q = expf((T == 1.f ? ld[e] : ld[e] / T) - info.Md) / info.Sd;
-        const float res = fmaxf(prob - q, 0.f);
-        any_res |= res > 0.f;
-        const float sr = res / Ee;
-        if (better(sr, idx, rv, ri)) {
-          rv = sr;
-          ri = idx;
-        }
-      }
-    }
+    body(v, l, E, ld);
   }
   block_argmax(pv, pi, shf, shi);
   Cand c{};
@@ -460,43 +526,39 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
   c.r_val = rv;
   c.r_idx = ri;
   c.any_res = any_res;
-  // The last workgroup of the sequence to finish merges the span candidates (counter zeroed by
-  // verify_decide).
-  __shared__ int last;
-  if (threadIdx.x == 0) {
-    p.cand[(int64_t)seq * p.nchunk + chunk] = c;
-    __threadfence();
-    last = atomicAdd(&p.done[seq], 1) == p.nchunk - 1;
-  }
-  __syncthreads();
-  if (!last || threadIdx.x != 0) return;
-  __threadfence();
-  finish_seq(p, seq, info);
+  if (threadIdx.x == 0) p.cand[(int64_t)seq * p.rchunk + chunk] = c;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct VLayout {
-  size_t stats, info, cand, done, total;
+  size_t stats, info, cand, total;
 };
 
-// Spans of a row: at most kSpans, a multiple of 4 entries each, none empty.
-void row_spans(int V, int* nchunk, int* span) {
-  const int n0 = min(kSpans, (V + 3) / 4);
+// Spans of a row: at most `most`, a multiple of 4 entries each, none empty.
+void spans_of(int V, int most, int* nchunk, int* span) {
+  const int n0 = std::max(1, std::min(most, (V + 3) / 4));
   *span = (((V + n0 - 1) / n0) + 3) / 4 * 4;
   *nchunk = (V + *span - 1) / *span;
 }
+// row_stats: at most kSpans per row (the table has S*(K+1) or more rows).
+void row_spans(int V, int* nchunk, int* span) { spans_of(V, kSpans, nchunk, span); }
+// verify_resample reads one target row per sequence (plus its draft row and noise): more spans per row, up
+// to about 2048 workgroups in all, so that a small batch still spreads over the GPU.
+void resample_spans(int S, int V, int* nchunk, int* span) {
+  spans_of(V, std::min(64, std::max(kSpans, (2048 + S - 1) / S)), nchunk, span);
+}
 
 VLayout verify_layout(int S, int K, int V, bool draft) {
-  int nchunk, span;
+  int nchunk, span, rchunk, rspan;
   row_spans(V, &nchunk, &span);
+  resample_spans(S, V, &rchunk, &rspan);
   const int64_t rows = (int64_t)S * (K + 1) + (draft ? (int64_t)S * K : 0);
   VLayout L;
   L.stats = 0;
   L.info = align256((size_t)rows * nchunk * sizeof(RowStat));
   L.cand = align256(L.info + (size_t)S * sizeof(SeqInfo));
-  L.done = align256(L.cand + (size_t)S * nchunk * sizeof(Cand));
-  L.total = align256(L.done + (size_t)S * sizeof(int32_t));
+  L.total = align256(L.cand + (size_t)S * rchunk * sizeof(Cand));
   return L;
 }
 
@@ -508,8 +570,10 @@ int launch_all(const VParams& p, hipStream_t s, bool draft) {
   if ((rc = check_launch("row_stats"))) return rc;
   hipLaunchKernelGGL((verify_decide<DT, DDT>), dim3(p.S), dim3(64), 0, s, p);
   if ((rc = check_launch("verify_decide"))) return rc;
-  hipLaunchKernelGGL((verify_resample<DT, DDT, kVec>), dim3(p.S, p.nchunk), dim3(kThreads), 0, s, p);
-  return check_launch("verify_resample");
+  hipLaunchKernelGGL((verify_resample<DT, DDT, kVec>), dim3(p.S, p.rchunk), dim3(kThreads), 0, s, p);
+  if ((rc = check_launch("verify_resample"))) return rc;
+  hipLaunchKernelGGL(verify_finish, dim3(p.S), dim3(kThreads), 0, s, p);
+  return check_launch("verify_finish");
 }
 
 int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
@@ -548,12 +612,12 @@ int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_
   p.K = K;
   p.V = V;
   row_spans(V, &p.nchunk, &p.span);
+  resample_spans(S, V, &p.rchunk, &p.rspan);
   p.out_a = out_a;
   p.out_next = out_next;
   p.stats = (RowStat*)((uint8_t*)workspace + lay.stats);
   p.info = (SeqInfo*)((uint8_t*)workspace + lay.info);
   p.cand = (Cand*)((uint8_t*)workspace + lay.cand);
-  p.done = (int32_t*)((uint8_t*)workspace + lay.done);
   hipStream_t s = (hipStream_t)stream;
   const bool lf = logits_dtype == SD_DTYPE_F32;
   const bool df = draft && draft_dtype == SD_DTYPE_F32;
