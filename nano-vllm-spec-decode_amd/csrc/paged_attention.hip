@@ -89,6 +89,7 @@ struct Params {
   int64_t out_stride;
   float* part_o;                // [item][Hkv][kResidues][rows_alloc][kD]
   float* part_ml;               // [item][Hkv][kResidues][rows_alloc][2] = (max, sum)
+  int32_t wave_slots;           // workgroups the GPU runs at once (one per CU): the head rotation period
 };
 
 struct Item {
@@ -483,10 +484,21 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   }
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs in linear order (residue group fastest, then KV
+// head, then item), so with 8 KV heads each XCD would run one head for the whole call. The heads' K/V
+// segments of a key row do not stream equally fast (on the headline call two heads ran ~15 % slower,
+// whichever XCD ran them), and that XCD's last workgroups then set the end of the call. The head is
+// therefore rotated by one per batch of workgroups the GPU holds at once: an XCD runs one head at a
+// time, a different one in each such batch (B=64 k=4: 193.7 -> 180.8 us).
+__device__ __forceinline__ int rotated_head(const Params& p, int y, int z) {
+  const int64_t linear = ((int64_t)z * gridDim.y + y) * gridDim.x;
+  return (int)((y + linear / p.wave_slots) % p.Hkv);
+}
+
 template <int RT, bool kVarlen, bool kPaged, int kWaves>
 __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes(kWaves)];
-  attn_body<RT, kVarlen, kPaged, kWaves>(p, lds, blockIdx.z, blockIdx.y, blockIdx.x);
+  attn_body<RT, kVarlen, kPaged, kWaves>(p, lds, blockIdx.z, rotated_head(p, blockIdx.y, blockIdx.z), blockIdx.x);
 }
 
 // A varlen call with long query runs: one launch for both work lists, so that the prefill q-blocks (MFMA
@@ -678,6 +690,19 @@ __global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __res
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// CUs of the current device (the number of 8-wave workgroups it runs at once), queried once per device.
+int wave_slots() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Layout {
@@ -825,6 +850,7 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
   Params p{};
+  p.wave_slots = wave_slots();
   p.q = (const uint16_t*)q;
   p.q_stride = q_token_stride;
   p.k = (const uint16_t*)k_cache;
@@ -958,6 +984,7 @@ int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_str
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
   Params p{};
+  p.wave_slots = wave_slots();
   p.q = (const uint16_t*)q;
   p.q_stride = q_token_stride;
   p.k = (const uint16_t*)k;
