@@ -517,7 +517,8 @@ static_assert(prefill::kThreads == kResidues * kWave, "both halves use 512-threa
 template <bool kPaged>
 __global__ __launch_bounds__(kResidues * kWave, 2) void mixed_fwd(Params p, PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kMixedLds];
-  const int h = blockIdx.x % a.Hkv;
+  // KV head fastest along the grid, rotated by one per batch of resident workgroups (see rotated_head).
+  const int h = (int)((blockIdx.x % a.Hkv + blockIdx.x / p.wave_slots) % a.Hkv);
   const int x = blockIdx.x / a.Hkv;
   const int np = *a.work_count, nr = *p.work_count;  // the plan's counts (each at most its grid share)
   constexpr int G = kMixedPre + kMixedRes;
