@@ -104,6 +104,38 @@ def bench_verify_attention(dev, steps, warmup, B=64, k=4, ctx_len=4096, W=33):
     return dict(bytes=nbytes, wall_s=wall, event_s=sum(ev) / len(ev), inputs=(q, kc, vc, lens, tables))
 
 
+def bench_verify_uniform(dev, B=64, k=4, lo=1024, hi=8192, W=33):
+    """Spec-verify attention with context lengths uniform in [lo, hi] (seeded), through the path
+    Attention.forward takes (sequences dispatched longest first, order planned once per step), graph-timed
+    over calls that each read the next of 3 cache copies; also the same call unplanned (index order)."""
+    import types
+    import numpy as np
+    import torch
+    from attn_cases import paged_cache, queries
+    from nanovllm_amd.layers.attention import paged_decode_attention
+    n = k + 1
+    ctx = np.random.default_rng(0).integers(lo, hi + 1, B).tolist()
+    kc, vc, tables = paged_cache(dev, ctx, HKV, D, W=W, seed=0)
+    caches = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(2)]
+    q = queries(dev, B * n, HQ, D, seed=1).view(B, n, HQ, D)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    out = torch.empty(B * n, HQ, D, dtype=torch.bfloat16, device=dev)
+    nbytes = decode_bytes(ctx, n)
+    res = {}
+    for name, owner in (("planned", types.SimpleNamespace()), ("unplanned", None)):
+        turn = [0]
+
+        def call():
+            a, b = caches[turn[0] % 3]
+            turn[0] += 1
+            paged_decode_attention(q, a, b, lens, tables, D ** -0.5, out=out, plan_owner=owner)
+        t = graph_timed(call, reps=12)
+        res[name] = dict(us=round(t * 1e6, 2), GBs=round(nbytes / t / 1e9, 1), frac=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4))
+    res["bytes"] = nbytes
+    res["contexts"] = f"uniform [{lo}, {hi}], seed 0, B={B}, k={k}"
+    return res
+
+
 def bench_store(dev, steps, warmup, N=2048, NB=4096):
     import torch
     from nanovllm_amd.layers.attention import store_kvcache
@@ -336,6 +368,7 @@ def main():
                      "bytes_per_launch": head["bytes"], "us_per_launch": round(t * 1e6, 2)},
     }
     if not args.skip_extras:
+        result["verify_attention_uniform_ctx"] = bench_verify_uniform(dev)
         result["kv_store"] = bench_store(dev, args.steps, args.warmup)
         result["verify_sampler"] = bench_sampler(dev, max(10, args.steps // 2), args.warmup)
         mixed = bench_mixed_attention(dev, max(5, args.steps // 10), 2)

@@ -62,8 +62,9 @@ int sd_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
  * softmax in increasing tile order and the eight residue partials are merged in residue order with a fixed
  * fma chain. That reduction depends only on key positions, so a row's result does not depend on num_seqs,
  * num_query_tokens or the other rows (bitwise), and equals the row's result from sd_varlen_attention.
- * The workspace (residue partials) is needed only when the call has too few (sequence, KV head) pairs to
- * merge inside one workgroup; sd_paged_decode_workspace_size returns 0 otherwise.
+ * sd_paged_decode needs the workspace only when the call has too few (sequence, KV head) pairs to merge
+ * inside one workgroup (residue partials); sd_paged_decode_workspace_size also counts the sequence order
+ * of the planned variant below.
  */
 size_t sd_paged_decode_workspace_size(int32_t num_seqs, int32_t num_query_tokens, int32_t num_heads,
                                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
@@ -74,6 +75,25 @@ int sd_paged_decode(const void* q, int64_t q_token_stride, const void* k_cache, 
                     int32_t num_query_tokens, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                     float scale, void* out, int64_t out_token_stride, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/*
+ * Decode / verify dispatch order, for callers that run many layers on one step's context lengths.
+ * sd_paged_decode takes the sequences in index order. sd_paged_decode_plan writes into `workspace` (sized by
+ * sd_paged_decode_workspace_size) the sequences sorted by context length, longest first (up to 1024
+ * sequences; index order beyond), and sd_paged_decode_planned (same arguments as sd_paged_decode) launches
+ * the workgroups in that order, so that long sequences do not end the call alone. The order only decides
+ * which workgroup computes which sequence: results are bitwise those of sd_paged_decode even when the
+ * plan was made for other context lengths, as long as it was made for the same num_seqs. No counterpart
+ * in the reference; it serves the per-layer loop of a decode step (nanovllm/engine/model_runner.py:476-485).
+ */
+int sd_paged_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_query_tokens, int32_t num_heads,
+                         int32_t num_kv_heads, void* workspace, size_t workspace_bytes, void* stream);
+int sd_paged_decode_planned(const void* q, int64_t q_token_stride, const void* k_cache, const void* v_cache,
+                            int64_t num_blocks, int32_t block_size, const int32_t* context_lens,
+                            const int32_t* block_tables, int32_t table_width, int32_t num_seqs,
+                            int32_t num_query_tokens, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                            float scale, void* out, int64_t out_token_stride, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /*
  * Varlen prefill / mixed prefill+decode attention. Replaces

@@ -74,6 +74,7 @@ struct Params {
   int32_t block_size;
   int64_t num_blocks;
   const int32_t* context_lens;  // decode
+  const int32_t* seq_order;     // decode: item i's sequence is seq_order[i / groups_per_seq] (null: i / groups)
   const int32_t* cu_q;          // varlen
   const int32_t* cu_k;          // varlen
   const int32_t* work;          // varlen: (sequence, group) pairs
@@ -113,7 +114,8 @@ __device__ __forceinline__ Item describe(const Params& p, int item) {
     if (it.q_start < 0 || it.Lq < 0 || it.q_start + it.Lq > p.total_q || it.Lk < 0) return it;
     if (!p.block_tables && (k0 < 0 || (int64_t)k0 + it.Lk > p.total_k)) return it;
   } else {
-    it.seq = item / p.groups_per_seq;
+    it.seq = p.seq_order ? p.seq_order[item / p.groups_per_seq] : item / p.groups_per_seq;
+    if (it.seq < 0 || (int64_t)it.seq * p.n >= p.total_q) return it;  // an order entry out of range
     grp = item % p.groups_per_seq;
     it.q_start = it.seq * p.n;
     it.Lq = p.n;
@@ -184,7 +186,8 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   int32_t blk_pre[kBlkPerThread];
   const int nblk_row = min(p.table_width, kMaxBlocks);
   if (kPaged && !kVarlen) {
-    const int seq = item / p.groups_per_seq;
+    int seq = p.seq_order ? p.seq_order[item / p.groups_per_seq] : item / p.groups_per_seq;
+    if (seq < 0 || (int64_t)seq * p.n >= p.total_q) seq = 0;  // describe() drops such an item
 #pragma unroll
     for (int i = 0; i < kBlkPerThread; ++i) {
       const int b = tid + i * kWaves * kWave;
@@ -689,6 +692,42 @@ __global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __res
   }
 }
 
+// Decode / verify order: the sequences by context length, longest first (ties by index), so that the
+// longest (sequence, KV head) workgroups are dispatched first and short ones fill the tail; up to
+// kPlanThreads sequences (more: index order). Any permutation gives the same results: only which workgroup
+// computes an item changes.
+__global__ __launch_bounds__(kPlanThreads) void decode_plan(const int32_t* __restrict__ context_lens, int32_t num_seqs,
+                                                            int32_t* __restrict__ order) {
+  __shared__ uint32_t keys[kPlanThreads];
+  const int tid = threadIdx.x;
+  if (num_seqs > kPlanThreads) {
+    for (int i = tid; i < num_seqs; i += kPlanThreads) order[i] = i;
+    return;
+  }
+  uint32_t key = 0xFFFFFFFFu;
+  if (tid < num_seqs) {
+    const int L = max(context_lens[tid], 0);
+    const uint32_t tiles = min((uint32_t)(L + kTile - 1) / kTile, (1u << 20) - 1);
+    key = (((1u << 20) - 1 - tiles) << 10) | (uint32_t)tid;
+  }
+  keys[tid] = key;
+  __syncthreads();
+  for (int k = 2; k <= kPlanThreads; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const int other = tid ^ j;
+      if (other > tid) {
+        const uint32_t a = keys[tid], b = keys[other];
+        if ((a > b) == ((tid & k) == 0)) {
+          keys[tid] = b;
+          keys[other] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (tid < num_seqs) order[tid] = (int32_t)(keys[tid] & 1023u);
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 // CUs of the current device (the number of 8-wave workgroups it runs at once), queried once per device.
@@ -707,12 +746,13 @@ int wave_slots() {
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Layout {
-  size_t part_o, part_ml, work, count, work_pre, count_pre, total;
+  size_t part_o, part_ml, work, count, work_pre, count_pre, order, total;
 };
 
 // Workspace: residue partials only when the merge runs in attn_combine (few items); for varlen, the two
 // work lists and their counts.
-Layout workspace_layout(int64_t items, int Hkv, int rows_alloc, bool partials, bool varlen, int64_t pre_items = 0) {
+Layout workspace_layout(int64_t items, int Hkv, int rows_alloc, bool partials, bool varlen, int64_t pre_items = 0,
+                        int64_t order_len = 0) {
   Layout L;
   const int64_t cells = partials ? items * Hkv * kResidues * rows_alloc : 0;
   L.part_o = 0;
@@ -721,7 +761,8 @@ Layout workspace_layout(int64_t items, int Hkv, int rows_alloc, bool partials, b
   L.count = align256(L.work + (varlen ? (size_t)items * 2 * sizeof(int32_t) : 0));
   L.work_pre = align256(L.count + (varlen ? sizeof(int32_t) : 0));
   L.count_pre = align256(L.work_pre + (varlen ? (size_t)pre_items * 2 * sizeof(int32_t) : 0));
-  L.total = align256(L.count_pre + (varlen ? sizeof(int32_t) : 0));
+  L.order = align256(L.count_pre + (varlen ? sizeof(int32_t) : 0));
+  L.total = align256(L.order + (size_t)order_len * sizeof(int32_t));
   return L;
 }
 
@@ -811,16 +852,15 @@ extern "C" size_t sd_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q
   decode_shape(num_query_tokens, num_heads / num_kv_heads, &RT, &P);
   const int64_t items = (int64_t)num_seqs * ((num_query_tokens + P - 1) / P);
   const bool partials = residue_waves(items, num_kv_heads, RT) < kResidues;
-  return workspace_layout(items, num_kv_heads, RT * 16, partials, false).total;
+  return workspace_layout(items, num_kv_heads, RT * 16, partials, false, 0, num_seqs).total;
 }
 
-extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void* k_cache, const void* v_cache,
-                               int64_t num_blocks, int32_t block_size, const int32_t* context_lens,
-                               const int32_t* block_tables, int32_t table_width, int32_t num_seqs,
-                               int32_t num_query_tokens, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                               float scale, void* out, int64_t out_token_stride, void* workspace,
-                               size_t workspace_bytes, void* stream) {
-  const char* who = "sd_paged_decode";
+namespace {
+int decode_run(const char* who, bool planned, const void* q, int64_t q_token_stride, const void* k_cache,
+               const void* v_cache, int64_t num_blocks, int32_t block_size, const int32_t* context_lens,
+               const int32_t* block_tables, int32_t table_width, int32_t num_seqs, int32_t num_query_tokens,
+               int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale, void* out,
+               int64_t out_token_stride, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_heads(who, num_heads, num_kv_heads, head_dim);
   if (rc) return rc;
   if (num_seqs < 0 || num_query_tokens <= 0 || table_width <= 0 || num_blocks <= 0)
@@ -846,9 +886,11 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
   if (items > 65535) return fail(kUnsupported, "%s: %lld work items exceed the grid limit", who, (long long)items);
   const int waves = residue_waves(items, num_kv_heads, RT);
   const bool partials = waves < kResidues;
-  const Layout lay = workspace_layout(items, num_kv_heads, RT * 16, partials, false);
-  if (partials && (!workspace || workspace_bytes < lay.total))
-    return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
+  const Layout lay = workspace_layout(items, num_kv_heads, RT * 16, partials, false, 0, num_seqs);
+  // The unplanned call needs the workspace only for partials; the planned one reads the order from it.
+  const size_t need = planned ? lay.total : partials ? lay.order : 0;
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, need);
 
   Params p{};
   p.wave_slots = wave_slots();
@@ -875,6 +917,7 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
   p.out_stride = out_token_stride;
   p.part_o = partials ? (float*)((uint8_t*)workspace + lay.part_o) : nullptr;
   p.part_ml = partials ? (float*)((uint8_t*)workspace + lay.part_ml) : nullptr;
+  p.seq_order = planned ? (const int32_t*)((uint8_t*)workspace + lay.order) : nullptr;
 
   hipStream_t s = (hipStream_t)stream;
   launch_fwd<false, true>(RT, waves, dim3(1, num_kv_heads, (unsigned)items), s, p);
@@ -884,6 +927,50 @@ extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void
     if ((rc = check_launch(who))) return rc;
   }
   return kOk;
+}
+}  // namespace
+
+extern "C" int sd_paged_decode(const void* q, int64_t q_token_stride, const void* k_cache, const void* v_cache,
+                               int64_t num_blocks, int32_t block_size, const int32_t* context_lens,
+                               const int32_t* block_tables, int32_t table_width, int32_t num_seqs,
+                               int32_t num_query_tokens, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                               float scale, void* out, int64_t out_token_stride, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  return decode_run("sd_paged_decode", false, q, q_token_stride, k_cache, v_cache, num_blocks, block_size,
+                    context_lens, block_tables, table_width, num_seqs, num_query_tokens, num_heads, num_kv_heads,
+                    head_dim, scale, out, out_token_stride, workspace, workspace_bytes, stream);
+}
+
+extern "C" int sd_paged_decode_planned(const void* q, int64_t q_token_stride, const void* k_cache,
+                                       const void* v_cache, int64_t num_blocks, int32_t block_size,
+                                       const int32_t* context_lens, const int32_t* block_tables, int32_t table_width,
+                                       int32_t num_seqs, int32_t num_query_tokens, int32_t num_heads,
+                                       int32_t num_kv_heads, int32_t head_dim, float scale, void* out,
+                                       int64_t out_token_stride, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+  return decode_run("sd_paged_decode_planned", true, q, q_token_stride, k_cache, v_cache, num_blocks, block_size,
+                    context_lens, block_tables, table_width, num_seqs, num_query_tokens, num_heads, num_kv_heads,
+                    head_dim, scale, out, out_token_stride, workspace, workspace_bytes, stream);
+}
+
+extern "C" int sd_paged_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_query_tokens,
+                                    int32_t num_heads, int32_t num_kv_heads, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  const char* who = "sd_paged_decode_plan";
+  if (num_seqs < 0 || num_query_tokens <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads)
+    return fail(kBadArgument, "%s: bad sizes", who);
+  if (num_seqs == 0) return kOk;
+  if (!context_lens) return fail(kBadArgument, "%s: null pointer", who);
+  int RT, P;
+  decode_shape(num_query_tokens, num_heads / num_kv_heads, &RT, &P);
+  const int64_t items = (int64_t)num_seqs * ((num_query_tokens + P - 1) / P);
+  const bool partials = residue_waves(items, num_kv_heads, RT) < kResidues;
+  const Layout lay = workspace_layout(items, num_kv_heads, RT * 16, partials, false, 0, num_seqs);
+  if (!workspace || workspace_bytes < lay.total)
+    return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
+  hipLaunchKernelGGL(decode_plan, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, context_lens, num_seqs,
+                     (int32_t*)((uint8_t*)workspace + lay.order));
+  return check_launch(who);
 }
 
 namespace {

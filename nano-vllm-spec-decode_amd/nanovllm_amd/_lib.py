@@ -26,6 +26,10 @@ SIGNATURES = {
     "sd_paged_decode_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "sd_paged_decode": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i32,
                                _i32, _i32, _i32, _i32, _f32, _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
+    "sd_paged_decode_plan": (_i32, [_c_void_p, _i32, _i32, _i32, _i32, _c_void_p, _size, _c_void_p]),
+    "sd_paged_decode_planned": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32,
+                                       _i32, _i32, _i32, _i32, _i32, _f32, _c_void_p, _i64, _c_void_p, _size,
+                                       _c_void_p]),
     "sd_varlen_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "sd_varlen_attention": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p,
                                    _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,

@@ -49,10 +49,20 @@ def _as_rows(x: torch.Tensor, heads: int, head_dim: int) -> torch.Tensor:
     return x
 
 
+# (owner, key) of the decode order held by the decode workspace (set by the last sd_paged_decode_plan call).
+_decode_plan_in_workspace = None
+
+
 def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            context_lens: torch.Tensor, block_tables: torch.Tensor, scale: float,
-                           out: torch.Tensor | None = None) -> torch.Tensor:
-    """q [B, n, Hq, D] -> [B*n, Hq, D]: flash_attn_with_kvcache(causal=True) semantics (attention.py:71-78)."""
+                           out: torch.Tensor | None = None, plan_owner: object | None = None) -> torch.Tensor:
+    """q [B, n, Hq, D] -> [B*n, Hq, D]: flash_attn_with_kvcache(causal=True) semantics (attention.py:71-78).
+
+    plan_owner: an object that lives as long as this context_lens (the step's Context). The sequences are
+    then dispatched longest first, in an order planned once per owner and batch shape and reused by later
+    layers (the order never changes results). A plan made while a graph is captured is only reused within
+    captures, one made eagerly only eagerly, so that every graph holds the plan it replays with."""
+    global _decode_plan_in_workspace
     B, n, Hq, hd = q.shape
     NB, bs, Hkv, _ = k_cache.shape
     _require(q.dtype == torch.bfloat16 and k_cache.dtype == torch.bfloat16, "paged_decode_attention: bf16 required")
@@ -65,10 +75,23 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     W = block_tables.size(1)
     lib = _lib.load()
     nbytes = lib.sd_paged_decode_workspace_size(B, n, Hq, Hkv, hd, bs, W)
-    ws = _lib.workspace(nbytes, q.device)
-    rc = lib.sd_paged_decode(qr.data_ptr(), qr.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), NB, bs,
-                             context_lens.data_ptr(), block_tables.data_ptr(), W, B, n, Hq, Hkv, hd, scale,
-                             out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _lib.stream_of(q.device))
+    ws = _lib.workspace(nbytes, q.device, tag="decode")
+    stream = _lib.stream_of(q.device)
+    fn = lib.sd_paged_decode
+    if plan_owner is not None and B > 0:
+        capturing = torch.cuda.is_current_stream_capturing()
+        key = (context_lens.data_ptr(), B, n, Hq, Hkv, ws.data_ptr(), ws.numel(), capturing)
+        cached = _decode_plan_in_workspace
+        if not (cached is not None and cached[0] is plan_owner and cached[1] == key):
+            _lib.check(lib.sd_paged_decode_plan(context_lens.data_ptr(), B, n, Hq, Hkv, ws.data_ptr(), ws.numel(),
+                                                stream), "sd_paged_decode_plan")
+            _decode_plan_in_workspace = (plan_owner, key)
+        fn = lib.sd_paged_decode_planned
+    else:
+        _decode_plan_in_workspace = None  # an unplanned call may write partials over the order
+    rc = fn(qr.data_ptr(), qr.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), NB, bs, context_lens.data_ptr(),
+            block_tables.data_ptr(), W, B, n, Hq, Hkv, hd, scale, out.data_ptr(), out.stride(0), ws.data_ptr(),
+            ws.numel(), stream)
     _lib.check(rc, "sd_paged_decode")
     return out
 
@@ -160,4 +183,5 @@ class Attention(nn.Module):
         # decode / verify: every sequence brings the same number of query tokens (1, or 1+k)
         num_seqs = context.context_lens.size(0)
         q = q.reshape(num_seqs, -1, self.num_heads, self.head_dim)
-        return paged_decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables, self.scale)
+        return paged_decode_attention(q, k_cache, v_cache, context.context_lens, context.block_tables, self.scale,
+                                      plan_owner=context)

@@ -137,3 +137,59 @@ def test_graph_capture_at_zero_lengths_then_replay(device):
         eager = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5)
         torch.cuda.synchronize()
         assert torch.equal(out, eager), it
+
+
+def test_planned_order_bitwise_and_stale_plan(device):
+    """The planned call (sequences dispatched longest first) equals the unplanned call bitwise, for small
+    and large batches (in-workgroup merge and partials + combine); a plan left from other context lengths of
+    the same batch size changes nothing either."""
+    from types import SimpleNamespace
+    from nanovllm_amd.layers import attention as att
+    rnd = random.Random(11)
+    for B, n in ((64, 5), (16, 9), (3, 2)):
+        ctx = [rnd.randint(1, 8192) for _ in range(B)]
+        kc, vc, tables = paged_cache(device, ctx, 8, 128, W=33, seed=60 + B)
+        q = queries(device, B * n, 32, 128, seed=61).view(B, n, 32, 128)
+        lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+        ref = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5)
+        owner = SimpleNamespace()
+        planned = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5, plan_owner=owner)
+        again = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5, plan_owner=owner)   # reused plan
+        assert torch.equal(planned, ref) and torch.equal(again, ref), B
+        # stale: plan for reversed lengths, then run with the real ones through the same owner and key
+        rev = torch.tensor(ctx[::-1], dtype=torch.int32, device=device)
+        lens.copy_(rev)
+        paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5, plan_owner=owner)
+        lens.copy_(torch.tensor(ctx, dtype=torch.int32, device=device))
+        stale = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5, plan_owner=owner)
+        assert att._decode_plan_in_workspace[0] is owner
+        assert torch.equal(stale, ref), B
+
+
+def test_planned_graph_capture_replays(device):
+    """Attention.forward's decode path (planned) captured at zero lengths, replayed with real metadata: the
+    graph holds the plan and equals the eager result bitwise on every replay."""
+    from nanovllm_amd.utils.context import Context
+    Hq, Hkv, D, W, n, B = 32, 8, 128, 33, 5, 32
+    rnd = random.Random(7)
+    kc, vc, _ = paged_cache(device, [8192] * B, Hkv, D, W=W, seed=71, extra_blocks=64)
+    q = torch.zeros(B, n, Hq, D, dtype=torch.bfloat16, device=device)
+    lens = torch.zeros(B, dtype=torch.int32, device=device)
+    tables = torch.zeros(B, W, dtype=torch.int32, device=device)
+    ctx_obj = Context(False, context_lens=lens, block_tables=tables)
+    out = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5, plan_owner=ctx_obj)   # warm-up
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5, plan_owner=ctx_obj)
+    NB = kc.size(0)
+    for it in range(3):
+        ctx = [rnd.randint(1, 8192) for _ in range(B)]
+        g = torch.Generator(device=device).manual_seed(80 + it)
+        q.copy_(queries(device, B * n, Hq, D, seed=90 + it).view(B, n, Hq, D))
+        lens.copy_(torch.tensor(ctx, dtype=torch.int32))
+        tables.copy_(torch.randperm(NB, device=device, generator=g)[:B * W].view(B, W).to(torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), it
