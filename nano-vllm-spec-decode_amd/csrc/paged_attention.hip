@@ -604,6 +604,30 @@ __device__ __forceinline__ int wave_inclusive_sum(int x, int lane) {
   return x;
 }
 
+// Ascending bitonic sort of keys[0, width) in LDS by the workgroup (width a power of two <= its size;
+// the padding keys 0xFFFFFFFF sort last). Narrow sorts (few sequences) take fewer barrier stages.
+__device__ __forceinline__ int sort_width(int n) {
+  int w = 64;
+  while (w < n) w <<= 1;
+  return w;
+}
+__device__ __forceinline__ void bitonic_sort(uint32_t* keys, int width) {
+  const int tid = threadIdx.x;
+  for (int k = 2; k <= width; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const int other = tid ^ j;
+      if (tid < width && other > tid) {
+        const uint32_t a = keys[tid], b = keys[other];
+        if ((a > b) == ((tid & k) == 0)) {
+          keys[tid] = b;
+          keys[other] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
 __global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __restrict__ cu_q,
                                                             const int32_t* __restrict__ cu_k, int32_t num_seqs,
                                                             int32_t P_res, int32_t P_pre,
@@ -628,19 +652,7 @@ __global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __res
     }
     keys[tid] = key;
     __syncthreads();
-    for (int k = 2; k <= kPlanThreads; k <<= 1) {
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        const int other = tid ^ j;
-        if (other > tid) {
-          const uint32_t a = keys[tid], b = keys[other];
-          if ((a > b) == ((tid & k) == 0)) {
-            keys[tid] = b;
-            keys[other] = a;
-          }
-        }
-        __syncthreads();
-      }
-    }
+    bitonic_sort(keys, sort_width(num_seqs));
   }
   __syncthreads();
   for (int base = 0; base < num_seqs; base += kPlanThreads) {
@@ -712,19 +724,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan(const int32_t* __res
   }
   keys[tid] = key;
   __syncthreads();
-  for (int k = 2; k <= kPlanThreads; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const int other = tid ^ j;
-      if (other > tid) {
-        const uint32_t a = keys[tid], b = keys[other];
-        if ((a > b) == ((tid & k) == 0)) {
-          keys[tid] = b;
-          keys[other] = a;
-        }
-      }
-      __syncthreads();
-    }
-  }
+  bitonic_sort(keys, sort_width(num_seqs));
   if (tid < num_seqs) order[tid] = (int32_t)(keys[tid] & 1023u);
 }
 
