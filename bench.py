@@ -152,6 +152,72 @@ def bench_store(dev, steps, warmup, N=2048, NB=4096):
     return dict(us=t * 1e6, GBs=nbytes / t / 1e9, bytes=nbytes, timing="graph replay of 20 calls")
 
 
+def norm_rope_bytes(N, write_k):
+    """Algorithmic bytes of one sd_qk_norm_rope_store call over N tokens with every slot valid: the qkv row,
+    the position, the fp32 cos / sin row and the slot per token; q out (and k out), the k / v cache rows."""
+    per_tok = (HQ + 2 * HKV) * D * 2 + 8 + D * 4 + 4 + HQ * D * 2 + (HKV * D * 2 if write_k else 0) + 2 * HKV * D * 2
+    return N * per_tok + 2 * D * 2
+
+
+def bench_qk_norm_rope(dev, N=2048, NB=4096, copies=12, max_pos=40960):
+    """Fused q/k RMSNorm + RoPE + KV store over one step's 2048 tokens (Qwen3-8B: 32 q / 8 kv heads, rope base
+    1e6), k read back from the cache only (mixed / decode steps), graph-timed over calls that each read the
+    next of `copies` qkv buffers (more bytes than the 256 MB last-level cache). Also the reference's
+    sequence of eager operations on this GPU (two RMSNorms, the rotation, the store) for comparison."""
+    import torch
+    from nanovllm_amd.layers.attention import store_kvcache
+    from nanovllm_amd.layers.rotary_embedding import RotaryEmbedding, qk_norm_rope_store
+    g = torch.Generator(device=dev).manual_seed(5)
+    W = (HQ + 2 * HKV) * D
+    qkvs = [torch.randn(N, W, device=dev, generator=g).to(torch.bfloat16) for _ in range(copies)]
+    pos = torch.randint(0, 4096, (N,), device=dev, generator=g)
+    slots = torch.randperm(NB * BLOCK, device=dev, generator=g)[:N].to(torch.int32)
+    rope = RotaryEmbedding(D, D, max_pos, 1e6).to(dev)
+    cs = rope.cos_sin_cache
+    qw = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(torch.bfloat16)
+    kc = torch.zeros(NB, BLOCK, HKV, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty(N, HQ, D, dtype=torch.bfloat16, device=dev)
+    turn = [0]
+
+    def split():
+        x = qkvs[turn[0] % copies]
+        turn[0] += 1
+        return (x[:, :HQ * D].view(N, HQ, D), x[:, HQ * D:(HQ + HKV) * D].view(N, HKV, D),
+                x[:, (HQ + HKV) * D:].view(N, HKV, D))
+
+    def fused():
+        q, k, v = split()
+        qk_norm_rope_store(pos, q, k, v, qw, kw, 1e-6, cs, kc, vc, slots, q_out=q_out, write_k=False)
+
+    def eager_norm(x, w):
+        xf = x.float()
+        var = xf.pow(2).mean(dim=-1, keepdim=True)
+        xf.mul_(torch.rsqrt(var + 1e-6))
+        return xf.to(torch.bfloat16).mul_(w)
+
+    cs3 = cs.view(max_pos, 1, D)
+
+    def eager_rot(x, cos, sin):
+        x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+    def unfused():
+        q, k, v = split()
+        q, k = eager_norm(q, qw), eager_norm(k, kw)
+        cos, sin = cs3[pos].chunk(2, dim=-1)
+        q, k = eager_rot(q, cos, sin), eager_rot(k, cos, sin)
+        store_kvcache(k, v, kc, vc, slots)
+
+    nbytes = norm_rope_bytes(N, write_k=False)
+    t = graph_timed(fused, reps=24)
+    te = graph_timed(unfused, reps=4)
+    return dict(us=round(t * 1e6, 2), GBs=round(nbytes / t / 1e9, 1), frac=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                bytes=nbytes, tokens=N, eager_reference_ops_us=round(te * 1e6, 1),
+                timing=f"graph replay of 24 calls over {copies} qkv buffers")
+
+
 def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
     import torch
     from nanovllm_amd.layers.sampler import verify_drafts
@@ -370,6 +436,7 @@ def main():
     if not args.skip_extras:
         result["verify_attention_uniform_ctx"] = bench_verify_uniform(dev)
         result["kv_store"] = bench_store(dev, args.steps, args.warmup)
+        result["qk_norm_rope_store"] = bench_qk_norm_rope(dev)
         result["verify_sampler"] = bench_sampler(dev, max(10, args.steps // 2), args.warmup)
         mixed = bench_mixed_attention(dev, max(5, args.steps // 10), 2)
         result["mixed_step_attention"] = mixed

@@ -52,6 +52,33 @@ int sd_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
                      int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim, void* stream);
 
 /*
+ * q/k RMSNorm + rotary embedding + KV store in one pass over a layer's qkv rows. Replaces, after the qkv
+ * split of Qwen3Attention.pre_attn (nanovllm/models/qwen3.py:89-96):
+ *   q_norm / k_norm  RMSNorm.rms_forward, nanovllm/layers/layernorm.py:16-26 (skipped when both weights are
+ *                    NULL: models with a qkv bias, qwen3.py:93);
+ *   rotary_emb       RotaryEmbedding.forward + apply_rotary_emb, nanovllm/layers/rotary_embedding.py:37-48,
+ *                    6-14 (neox halves, fp32 cos / sin);
+ *   store_kvcache    nanovllm/layers/attention.py:33-40 as Attention.forward calls it (:62-63), when the
+ *                    caches are given (then Attention.forward must not store again).
+ * q [tokens, num_heads, head_dim], k / v [tokens, num_kv_heads, head_dim] bf16 with the given row strides
+ * (views of one qkv row work); positions int64 [tokens]; norm weights bf16 [head_dim]; cos_sin_cache fp32
+ * [max_position, head_dim] (cos of the head_dim/2 frequencies, then sin: the reference's cos_sin_cache
+ * buffer). Writes q_out (may be q itself) and, if k_out is not NULL, k_out (may be k). With k_cache /
+ * v_cache (both or neither, [num_slots, num_kv_heads*head_dim] bf16) the rotated k and the unchanged v
+ * rows go to slot slot_mapping[t]; negative slots and slots >= num_slots are skipped.
+ * Arithmetic: fp32, correctly rounded 1/sqrt(mean(x^2) + eps), bf16 rounding after the normalisation,
+ * after the weight and after the rotation, as the reference's eager operations. A position outside
+ * [0, max_position) gives NaN rows for that token. head_dim 128 only.
+ */
+int sd_qk_norm_rope_store(const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride,
+                          const void* v, int64_t v_row_stride, const int64_t* positions, const void* q_norm_weight,
+                          const void* k_norm_weight, float eps, const float* cos_sin_cache, int64_t max_position,
+                          void* q_out, int64_t q_out_row_stride, void* k_out, int64_t k_out_row_stride,
+                          void* k_cache, void* v_cache, int64_t num_slots, const int32_t* slot_mapping,
+                          int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                          void* stream);
+
+/*
  * Decode / speculative-verify attention over the paged cache. Replaces
  * flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=context_lens, block_table=block_tables,
  * softmax_scale=scale, causal=True), nanovllm/layers/attention.py:71-78.

@@ -23,6 +23,9 @@ SIGNATURES = {
     "sd_last_error": (ctypes.c_char_p, []),
     "sd_store_kvcache": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i32, _i32,
                                 _i32, _c_void_p]),
+    "sd_qk_norm_rope_store": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p,
+                                     _c_void_p, _f32, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _c_void_p,
+                                     _c_void_p, _i64, _c_void_p, _i32, _i32, _i32, _i32, _c_void_p]),
     "sd_paged_decode_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "sd_paged_decode": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i32,
                                _i32, _i32, _i32, _i32, _f32, _c_void_p, _i64, _c_void_p, _size, _c_void_p]),

@@ -26,7 +26,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared_functions()
-    assert len(names) == 14, names
+    assert len(names) == 15, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -73,6 +73,21 @@ def test_bad_arguments_return_status(lib):
                               ctypes.addressof(ws), None, 0, 0, None, None, 2, 1, 10, ctypes.addressof(ws),
                               ctypes.addressof(ws), ctypes.addressof(ws), 16, None)
     assert rc == 2 and b"dtype" in lib.sd_last_error()
+    nr = lib.sd_qk_norm_rope_store
+    rc = nr(None, 4096, None, 1024, None, 1024, None, None, None, 1e-6, None, 100, None, 4096, None, 0, None, None,
+            0, None, 4, 32, 8, 64, None)
+    assert rc == 2 and b"head_dim 64" in lib.sd_last_error()
+    rc = nr(None, 4096, None, 1024, None, 1024, None, ctypes.addressof(ws), None, 1e-6, None, 100, None, 4096, None,
+            0, None, None, 0, None, 4, 32, 8, 128, None)
+    assert rc == 1 and b"both norm weights" in lib.sd_last_error()
+    rc = nr(None, 4096, None, 1024, None, 1024, None, None, None, 1e-6, None, 100, None, 4096, None, 0,
+            ctypes.addressof(ws), None, 0, None, 4, 32, 8, 128, None)
+    assert rc == 1 and b"store needs" in lib.sd_last_error()
+    rc = nr(None, 4096, None, 1024, None, 1024, None, None, None, -1.0, None, 100, None, 4096, None, 0, None, None,
+            0, None, 4, 32, 8, 128, None)
+    assert rc == 1 and b"eps" in lib.sd_last_error()
+    assert nr(None, 0, None, 0, None, 0, None, None, None, 1e-6, None, 100, None, 0, None, 0, None, None, 0, None,
+              0, 32, 8, 128, None) == 0                                                    # nothing to do
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
