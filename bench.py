@@ -218,6 +218,34 @@ def bench_qk_norm_rope(dev, N=2048, NB=4096, copies=12, max_pos=40960):
                 timing=f"graph replay of 24 calls over {copies} qkv buffers")
 
 
+def bench_draft_inputs(dev, B=64, W=33):
+    """One later draft step's inputs for 64 sequences (sd_draft_step_inputs, one launch) against the
+    reference's tensor operations for the same step on this GPU (model_runner.py:446-452), both graph-timed."""
+    import torch
+    from nanovllm_amd.engine.draft_inputs import DraftStepBuffers, draft_step_inputs
+    g = torch.Generator(device=dev).manual_seed(6)
+    real_lens = torch.randint(1024, 8192, (B,), device=dev, generator=g).to(torch.int32)
+    last_pos = real_lens.long() - 1
+    tables = torch.randperm(4096, device=dev, generator=g)[:B * W].view(B, W).to(torch.int32)
+    tokens = torch.randint(0, 151936, (B,), device=dev, generator=g)
+    bufs = DraftStepBuffers(B, dev)
+    input_ids = torch.zeros(B, dtype=torch.int64, device=dev)
+
+    def reference_ops():
+        real = real_lens > 0
+        pos = torch.where(real, last_pos + 1, 0)
+        block = tables.gather(1, (pos // BLOCK).unsqueeze(1)).squeeze(1)
+        slot = torch.where(real, block * BLOCK + pos % BLOCK, -1).to(torch.int32)
+        lens = torch.where(real, pos + 1, 0).to(torch.int32)
+        input_ids[:B] = tokens
+        return pos, slot, lens
+
+    t = graph_timed(lambda: draft_step_inputs(real_lens, last_pos, tables, BLOCK, tokens, 1, bufs), reps=20)
+    tr = graph_timed(reference_ops, reps=20)
+    return dict(us=round(t * 1e6, 2), reference_ops_us=round(tr * 1e6, 2), seqs=B,
+                timing="graph replay of 20 calls (one launch against the reference's ten operations)")
+
+
 def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
     import torch
     from nanovllm_amd.layers.sampler import verify_drafts
@@ -437,6 +465,7 @@ def main():
         result["verify_attention_uniform_ctx"] = bench_verify_uniform(dev)
         result["kv_store"] = bench_store(dev, args.steps, args.warmup)
         result["qk_norm_rope_store"] = bench_qk_norm_rope(dev)
+        result["draft_step_inputs"] = bench_draft_inputs(dev)
         result["verify_sampler"] = bench_sampler(dev, max(10, args.steps // 2), args.warmup)
         mixed = bench_mixed_attention(dev, max(5, args.steps // 10), 2)
         result["mixed_step_attention"] = mixed

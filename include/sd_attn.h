@@ -187,6 +187,23 @@ int sd_verify_drafts(const void* logits, int32_t logits_dtype, int64_t logits_ro
                      size_t workspace_bytes, void* stream);
 
 /*
+ * Inputs of one later draft step. Replaces the tensor operations of ModelRunner.run_draft's loop,
+ * nanovllm/engine/model_runner.py:443-452 (steps j = 1 .. k-1). For every sequence b < num_seqs:
+ *   real = real_lens[b] > 0 (the first draft step's context_lens; 0 marks a padding sequence)
+ *   positions[b]    = real ? last_positions[b] + step : 0
+ *   slot_mapping[b] = real ? block_tables[b, pos / block_size] * block_size + pos % block_size : -1
+ *   context_lens[b] = real ? pos + 1 : 0
+ *   input_ids[b]    = b < num_tokens ? tokens[b] : 0   (tokens: the last sampled draft tokens, int64 [S])
+ * Integer results equal the reference's (int64 arithmetic, int32 outputs truncated as torch's casts do).
+ * Where the reference's gather would index past the block table (pos / block_size >= table_width), the
+ * slot is -1 instead of a device fault. One launch; every output element is written.
+ */
+int sd_draft_step_inputs(const int32_t* real_lens, const int64_t* last_positions, const int32_t* block_tables,
+                         int32_t table_width, int32_t block_size, const int64_t* tokens, int32_t num_tokens,
+                         int32_t step, int32_t num_seqs, int64_t* input_ids, int64_t* positions,
+                         int32_t* slot_mapping, int32_t* context_lens, void* stream);
+
+/*
  * Token sampler. Replaces Sampler.forward(logits, temperatures), nanovllm/layers/sampler.py:5-16, with
  * the internal exponential_(1) noise passed in as exp_noise fp32 [S, vocab] (NULL if all greedy).
  * Greedy rows (temperature 0) take the first argmax; the others argmax(softmax(l/T) / max(E, 1e-10)).

@@ -26,7 +26,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared_functions()
-    assert len(names) == 15, names
+    assert len(names) == 16, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -88,6 +88,12 @@ def test_bad_arguments_return_status(lib):
     assert rc == 1 and b"eps" in lib.sd_last_error()
     assert nr(None, 0, None, 0, None, 0, None, None, None, 1e-6, None, 100, None, 0, None, 0, None, None, 0, None,
               0, 32, 8, 128, None) == 0                                                    # nothing to do
+    di = lib.sd_draft_step_inputs
+    rc = di(None, None, None, 33, 256, None, 5, 1, 4, None, None, None, None, None)
+    assert rc == 1 and b"bad sizes" in lib.sd_last_error()                   # more tokens than sequences
+    rc = di(None, None, None, 33, 256, None, 0, 1, 4, None, None, None, None, None)
+    assert rc == 1 and b"null pointer" in lib.sd_last_error()
+    assert di(None, None, None, 33, 256, None, 0, 1, 0, None, None, None, None, None) == 0  # nothing to do
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

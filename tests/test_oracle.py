@@ -328,3 +328,33 @@ def test_sample_closed_form():
     a, t = osmp.verify_drafts(logits, torch.zeros(S, 0, dtype=torch.int64), torch.zeros(S, dtype=torch.int64), temps,
                               uniforms=torch.zeros(S, 0), exp_noise=e)
     assert torch.equal(t, got) and a.tolist() == [0] * S
+
+
+# ------------------------------------------------------------------ draft-step inputs
+
+def test_draft_step_inputs_bruteforce():
+    """Per-sequence loop in plain Python (model_runner.py:446-452 read one sequence at a time): padding
+    sequences (context length 0) get position 0, slot -1, length 0; block boundaries cross to the next
+    table entry; rows past S keep input id 0."""
+    from oracle import draft_inputs as odi
+    g = torch.Generator().manual_seed(9)
+    B, S, W, bs = 12, 9, 5, 16
+    tables = torch.randperm(100, generator=g)[:B * W].view(B, W).to(torch.int32)
+    real_lens = torch.tensor([5, 17, 0, 31, 1, 64, 16, 0, 33, 2, 47, 0], dtype=torch.int32)
+    last_pos = torch.tensor([3, 15, 7, 30, 0, 60, 14, 0, 31, 0, 45, 2], dtype=torch.int64)
+    tokens = torch.randint(0, 1000, (S,), generator=g)
+    for j in (1, 2, 3):
+        ids, pos, slots, lens = odi.draft_step_inputs(real_lens, last_pos, tables, bs, tokens, j)
+        assert ids.dtype == torch.int64 and pos.dtype == torch.int64
+        assert slots.dtype == torch.int32 and lens.dtype == torch.int32
+        for b in range(B):
+            if int(real_lens[b]) > 0:
+                p = int(last_pos[b]) + j
+                assert int(pos[b]) == p and int(lens[b]) == p + 1
+                assert int(slots[b]) == int(tables[b, p // bs]) * bs + p % bs
+            else:
+                assert int(pos[b]) == 0 and int(slots[b]) == -1 and int(lens[b]) == 0
+            assert int(ids[b]) == (int(tokens[b]) if b < S else 0)
+    # position 15 + 1 = 16 is the first slot of the second block
+    _, pos, slots, _ = odi.draft_step_inputs(real_lens, last_pos, tables, bs, tokens, 1)
+    assert int(pos[1]) == 16 and int(slots[1]) == int(tables[1, 1]) * bs
