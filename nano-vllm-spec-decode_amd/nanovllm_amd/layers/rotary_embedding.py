@@ -36,10 +36,10 @@ def qk_norm_rope_store(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor
     """q [N, Hq, D], k / v [N, Hkv, D] bf16 (views of the qkv split are fine) -> (q, k) after
     RMSNorm (weights None: none, the qkv-bias models of qwen3.py:93) and the rotary embedding.
 
-    With k_cache / v_cache ([NB, block_size, Hkv, D], the Attention module's caches) and slot_mapping, the
-    rotated k and v are also stored (slot -1 skipped); the caller then passes kv_stored=True to
-    Attention.forward. q_out / k_out default to new tensors; pass q / k for in place. write_k=False skips
-    k_out (decode steps read k from the cache only) and returns None for it."""
+    With k_cache / v_cache ([NB, block_size, Hkv, D], the Attention module's caches; None or empty: no store)
+    and slot_mapping, the rotated k and v are also stored (slot -1 skipped); the caller then passes
+    kv_stored=True to Attention.forward. q_out / k_out default to new tensors; pass q / k for in place.
+    write_k=False skips k_out (decode steps read k from the cache only) and returns None for it."""
     q, k = _heads(q, "q"), _heads(k, "k")
     N, Hq, D = q.shape
     Hkv = k.size(1)
@@ -55,9 +55,10 @@ def qk_norm_rope_store(positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor
         for w in (q_norm_weight, k_norm_weight):
             _require(w.dtype == torch.bfloat16 and w.is_contiguous() and w.numel() == D,
                      "norm weights: bf16 [head_dim] required")
-    store = k_cache is not None
+    # empty caches (before the KV cache is allocated) store nothing, as attention.py:62 skips the store
+    store = k_cache is not None and k_cache.numel() > 0 and v_cache is not None and v_cache.numel() > 0
     if store:
-        _require(v is not None and v_cache is not None and slot_mapping is not None, "store needs v, v_cache, slots")
+        _require(v is not None and slot_mapping is not None, "store needs v and slot_mapping")
         v = _heads(v, "v")
         _require(v.shape == k.shape, "v: shape mismatch with k")
         _require(k_cache.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16 and k_cache.is_contiguous()
