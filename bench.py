@@ -8,12 +8,18 @@ the outputs, the block-table entries and context lengths) divided by the measure
 launch that rocprofv3's FETCH_SIZE + WRITE_SIZE counters measured for this launch (committed summary under
 profiles/), null if that summary is absent.
 
-Also reported (same JSON line): the KV-cache scatter (2048 rows, 10% padding slots), the rejection sampler
-(S 64, K 4, V 151936, T 0 and T 1 with draft logits) and a 2048-token mixed prefill+decode attention step
-over 36 layers replayed as one HIP graph by the mixed-step runtime (tok/s), plus a CPU baseline: the oracle (PyTorch CPU restatement) timed on the headline
-workload for about 10 s on 16 host threads.
+Also reported (same JSON line):
+* the KV-cache scatter (2048 rows, 10% padding slots);
+* the fused q/k RMSNorm + RoPE + KV store over 2048 tokens, next to the reference's eager operations;
+* one draft step's inputs for 64 sequences, next to the reference's tensor operations;
+* the rejection sampler (S 64, K 4, V 151936, T 0 and T 1 with draft logits);
+* a 2048-token mixed prefill+decode attention step over 36 layers, replayed as one HIP graph by the mixed-step
+  runtime (tok/s), and the prefill kernel at GPU-filling sizes;
+* a CPU baseline: the oracle (PyTorch CPU restatement) timed on the headline workload for about 10 s on 16
+  host threads.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+    python bench.py --only qk_norm_rope_store      (one secondary workload alone, for profiling)
 """
 import argparse
 import json
@@ -420,6 +426,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-extras", action="store_true", help="headline only (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="leave out the CPU baseline (for profiling)")
+    ap.add_argument("--only", choices=["qk_norm_rope_store", "draft_step_inputs", "kv_store"],
+                    help="run one secondary workload alone and print its JSON (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -436,6 +444,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.only:
+        fn = {"qk_norm_rope_store": lambda: bench_qk_norm_rope(dev), "draft_step_inputs": lambda: bench_draft_inputs(dev),
+              "kv_store": lambda: bench_store(dev, args.steps, args.warmup)}[args.only]
+        print(json.dumps({args.only: fn()}), flush=True)
+        return
     head = bench_verify_attention(dev, args.steps, args.warmup)
     t = head["event_s"]
     achieved = head["bytes"] / t / 1e9
