@@ -404,7 +404,45 @@ def cpu_baseline(inputs, min_seconds=10.0, max_reps=8):
     nbytes = decode_bytes(ls.tolist(), q.size(1))
     return dict(value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(), kind="port",
                 sample=f"the full headline call (64 sequences, ctx 4096, k=4) through the oracle's "
-                       f"paged_decode_attention, {reps} runs, {total:.1f} s total, {t * 1e3:.0f} ms per call")
+                       f"paged_decode_attention, {reps} runs, {total:.1f} s total, {t * 1e3:.0f} ms per call",
+                secondary=cpu_secondary())
+
+
+def cpu_secondary(reps=3):
+    """The oracle on the secondary workloads' shapes (same threads): the fused q/k norm + RoPE + store over 2048
+    tokens and one draft step's inputs for 64 sequences; milliseconds per call, best of `reps`."""
+    import torch
+    from oracle import draft_inputs as odi
+    from oracle import qk_norm_rope as onr
+    g = torch.Generator().manual_seed(7)
+    N, NB, W = 2048, 512, 33
+    qkv = torch.randn(N, (HQ + 2 * HKV) * D, generator=g).to(torch.bfloat16)
+    q = qkv[:, :HQ * D].view(N, HQ, D)
+    k = qkv[:, HQ * D:(HQ + HKV) * D].view(N, HKV, D)
+    v = qkv[:, (HQ + HKV) * D:].view(N, HKV, D)
+    pos = torch.randint(0, 4096, (N,), generator=g)
+    cs = onr.rope_cache(D, 40960, 1e6)
+    w = torch.ones(D, dtype=torch.bfloat16)
+    slots = torch.randperm(NB * BLOCK, generator=g)[:N].to(torch.int32)
+    kc = torch.zeros(NB, BLOCK, HKV, D, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    real = torch.randint(1024, 8192, (64,), generator=g).to(torch.int32)
+    last = real.long() - 1
+    tables = torch.randperm(4096, generator=g)[:64 * W].view(64, W).to(torch.int32)
+    toks = torch.randint(0, 151936, (64,), generator=g)
+    out = {}
+    for name, fn in (("qk_norm_rope_store_2048_tokens_ms",
+                      lambda: onr.qk_norm_rope_store(q, k, v, pos, w, w, 1e-6, cs, kc, vc, slots)),
+                     ("draft_step_inputs_64_seqs_ms",
+                      lambda: odi.draft_step_inputs(real, last, tables, BLOCK, toks, 1))):
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            best = min(best, time.perf_counter() - t0)
+        out[name] = round(best * 1e3, 3)
+    del kc, vc
+    return out
 
 
 def pmc_traffic(path=os.path.join(ROOT, "profiles", "attn_fwd_verify_b64_k4_ctx4096.pmc.txt")):

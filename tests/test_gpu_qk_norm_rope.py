@@ -100,7 +100,8 @@ def _check_caches(res, slots, Hkv):
     assert not touched[keep].any()
 
 
-@pytest.mark.parametrize("N,Hq,Hkv", [(1, 32, 8), (7, 32, 8), (64, 32, 8), (2048, 32, 8), (20, 16, 8)])
+# (28, 4): 36 heads per token, so the 8-lane groups of one wave mix q, k and v heads of two tokens.
+@pytest.mark.parametrize("N,Hq,Hkv", [(1, 32, 8), (7, 32, 8), (64, 32, 8), (2048, 32, 8), (20, 16, 8), (33, 28, 4)])
 def test_norm_rope_store_vs_oracle(device, N, Hq, Hkv):
     print(f"case N={N} Hq={Hq} Hkv={Hkv}", flush=True)
     c = _case(device, N, Hq, Hkv, seed=N + Hq)
@@ -121,12 +122,24 @@ def test_norm_bitexact_when_sum_is_exact(device):
     _check_caches(res, c["slots"], 8)
 
 
-def test_rope_only_bitexact(device):
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (28, 4)])
+def test_rope_only_bitexact(device, Hq, Hkv):
     """No norm (models with a qkv bias) and no store: the rotation alone is bit-exact."""
-    c = _case(device, 300, 32, 8, seed=12)
+    c = _case(device, 300, Hq, Hkv, seed=12)
     res = _run_both(c, norm=False, store=False)
     assert torch.equal(_bits(res["q"]), _bits(res["eq"]))
     assert torch.equal(_bits(res["k"]), _bits(res["ek"]))
+
+
+def test_rope_only_with_store_bitexact(device):
+    """Rotation without the norm but with the store (qkv-bias models in the fused path): bit-exact, and the
+    caches hold the rotated k and the unchanged v."""
+    c = _case(device, 129, 28, 4, seed=19)
+    res = _run_both(c, norm=False, store=True)
+    assert torch.equal(_bits(res["q"]), _bits(res["eq"]))
+    assert torch.equal(_bits(res["k"]), _bits(res["ek"]))
+    assert torch.equal(_bits(res["kc"]), _bits(res["ekc"])) and torch.equal(_bits(res["vc"]), _bits(res["evc"]))
+    _check_caches(res, c["slots"], 4)
 
 
 def test_in_place_and_no_k_out(device):
