@@ -504,6 +504,259 @@ __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Para
   attn_body<RT, kVarlen, kPaged, kWaves>(p, lds, blockIdx.z, rotated_head(p, blockIdx.y, blockIdx.z), blockIdx.x);
 }
 
+// Few (item, KV head) pairs (one-residue workgroups): the residue body with one wave keeps one 16 KB tile in
+// flight and does each tile's math in one dependent chain, so such calls are bounded by latency. Here one
+// wave streams the residue's tiles (three in registers, one ahead in a two-slot LDS ring, one barrier per
+// tile) and four waves share the math: each takes one 16-row tile and a range of the 8 d-tiles of O (its
+// rows' scores and softmax are computed by every wave that shares the row tile, identically). Rows and d
+// columns are independent, so every output element goes through exactly the arithmetic of attn_body with
+// one wave, in the same order: the partials written for attn_combine, and the results, are bitwise the
+// same. The barriers wait for LDS only (prefill::block_sync), so the streaming wave's loads stay in flight
+// across them.
+constexpr int kStreamDepth = 3;                 // tiles in the streaming wave's registers
+constexpr int kStreamMath = 4;                  // waves that do the math
+constexpr int kStreamThreads = (kStreamMath + 1) * kWave;
+constexpr int kSlotBytes = 2 * kVBuf;           // one K and one V tile
+constexpr int kStreamLds = 2 * kSlotBytes + kMaxBlocks * 4;
+
+template <int RT, bool kVarlen, bool kPaged>
+__device__ __forceinline__ void stream_body(const Params& p, uint8_t* lds, int item, int h, int residue) {
+  // Math wave c: row tile c / per_rt, d-tiles (c % per_rt) * DT .. +DT-1 (three row tiles: one each, wave 3
+  // idle).
+  constexpr int kPerRt = RT == 3 ? 1 : kStreamMath / RT;
+  constexpr int DT = 8 / kPerRt;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const bool loader = wave == kStreamMath;
+  const int lane = tid % kWave;
+  const int r16 = lane % 16;
+  const int grp = lane / 16;
+  int32_t* blk_ids = (int32_t*)(lds + 2 * kSlotBytes);
+
+  const Item it = describe<kVarlen>(p, item);
+  if (!it.valid) return;
+  const int rows = it.np * p.g;
+  const int kmax = it.kmax;
+  const int end_tile = (kmax + kTile - 1) / kTile;
+  const int nblk_row = min(p.table_width, kMaxBlocks);
+  if (kPaged) {
+    for (int b = tid; b < nblk_row; b += kStreamThreads)
+      blk_ids[b] = p.block_tables[(int64_t)it.seq * p.table_width + b];
+    __syncthreads();
+  }
+  const int steps = residue < end_tile ? (end_tile - residue + kResidues - 1) / kResidues : 0;
+
+  struct TileSrc {
+    const uint8_t* kb;
+    const uint8_t* vb;
+    int nvalid;
+    bool ok;
+  };
+  const int64_t ksb = p.k_stride * 2, vsb = p.v_stride * 2;
+  // Tile jt's K / V base (past the last tile: the item's first tile, loaded and never read).
+  auto tile_src = [&](int jt) {
+    TileSrc ts;
+    if (jt >= end_tile) jt = 0;
+    const int t0 = jt * kTile;
+    ts.nvalid = min(kTile, kmax - t0);
+    ts.ok = true;
+    int64_t row0;
+    if (kPaged) {
+      const int bi = t0 / p.block_size;
+      const int blk = __builtin_amdgcn_readfirstlane(bi < nblk_row ? blk_ids[bi] : -1);
+      ts.ok = blk >= 0 && blk < p.num_blocks;
+      row0 = (int64_t)(ts.ok ? blk : 0) * p.block_size + t0 % p.block_size;
+    } else {
+      row0 = (int64_t)p.cu_k[it.seq] + t0;
+    }
+    ts.kb = (const uint8_t*)p.k + row0 * ksb + h * kD * 2;
+    ts.vb = (const uint8_t*)p.v + row0 * vsb + h * kD * 2;
+    return ts;
+  };
+  auto slot_k = [&](int s) { return lds + (s % 2) * kSlotBytes; };
+  auto slot_v = [&](int s) { return lds + (s % 2) * kSlotBytes + kVBuf; };
+
+  if (loader) {
+    // ---- the streaming wave: K in the math waves' register layout (key 16*kt + r16, d = 32*ks + 8*grp + e;
+    // keys past the tile's end read its first key), V in the residue body's LDS layout ----
+    const uint32_t k_off0 = (uint32_t)(r16 * ksb) + 16 * grp;
+    const uint32_t k_off1 = k_off0 + (uint32_t)(16 * ksb);
+    const int vf_key = lane / 16;
+    const int vf_slot = lane % 16;
+    const uint32_t v_c0 = 16 * (vf_slot ^ (2 * vf_key)), v_c1 = 16 * (vf_slot ^ (2 * (4 + vf_key)));
+    const uint32_t v_off0 = (uint32_t)(vf_key * vsb) + v_c0, v_off1 = (uint32_t)(vf_key * vsb) + v_c1;
+    struct Regs {
+      u32x4 k[8], v[8];
+      bool ok;
+    };
+    auto load = [&](int s, Regs& r) {
+      const TileSrc ts = tile_src(residue + kResidues * s);
+      const uint32_t off0 = r16 < ts.nvalid ? k_off0 : 16 * grp;
+      const uint32_t off1 = 16 + r16 < ts.nvalid ? k_off1 : 16 * grp;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        r.k[ks] = *(const u32x4*)(ts.kb + off0 + 64 * ks);
+        r.k[4 + ks] = *(const u32x4*)(ts.kb + off1 + 64 * ks);
+      }
+#pragma unroll
+      for (int qd = 0; qd < 8; ++qd) {
+        const bool valid = 4 * qd + vf_key < ts.nvalid;
+        const uint32_t off = (qd % 2) ? (valid ? v_off1 : v_c1) : (valid ? v_off0 : v_c0);
+        r.v[qd] = *(const u32x4*)(ts.vb + (valid ? (int64_t)(4 * qd) * vsb : 0) + off);
+      }
+      r.ok = ts.ok;
+    };
+    auto store = [&](int s, const Regs& r) {
+      uint8_t* kd = slot_k(s) + 16 * lane;
+      uint8_t* vd = slot_v(s) + 16 * lane;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) *(u32x4*)(kd + 1024 * i) = r.k[i];
+#pragma unroll
+      for (int qd = 0; qd < 8; ++qd) *(u32x4*)(vd + 1024 * qd) = r.ok ? r.v[qd] : u32x4{0, 0, 0, 0};
+    };
+    Regs ra, rb, rc;
+    if (steps > 0) {
+      load(0, ra);
+      load(1, rb);
+      load(2, rc);
+      store(0, ra);
+      load(3, ra);
+    }
+    prefill::block_sync();
+    // Steps in threes so that every register set is static: tile s+1 is stored while the math waves work
+    // on tile s, then tile s+4 is loaded into the freed set. Past the last step, loads and stores are of
+    // valid addresses and never read.
+    for (int s = 0; s < steps; s += kStreamDepth) {
+      store(s + 1, rb);
+      load(s + 4, rb);
+      prefill::block_sync();
+      if (s + 1 >= steps) break;
+      store(s + 2, rc);
+      load(s + 5, rc);
+      prefill::block_sync();
+      if (s + 2 >= steps) break;
+      store(s + 3, ra);
+      load(s + 6, ra);
+      prefill::block_sync();
+    }
+    return;
+  }
+
+  // ---- a math wave: the residue body's arithmetic for one row tile and DT d-tiles ----
+  const bool idle = wave >= RT * kPerRt;   // three row tiles: the fourth wave only keeps the barriers
+  const int rt = idle ? 0 : wave / kPerRt;
+  const int dt0 = (wave % kPerRt) * DT;
+  const int row = rt * 16 + r16;
+  int lim;
+  bf16x8 qv[4];
+  if (row < rows) {
+    const int i = it.p0 + row / p.g;
+    const int hq = h * p.g + row % p.g;
+    lim = min(max(it.Lk - it.Lq + i + 1, 0), kmax);
+    const uint16_t* qp = p.q + (int64_t)(it.q_start + i) * p.q_stride + hq * kD + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qv[ks] = *(const bf16x8*)(qp + 32 * ks);
+  } else {
+    lim = kmax;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qv[ks] = bf16x8{};
+  }
+  float m = -INFINITY, l = 0.f;
+  f32x4 o[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) o[d] = f32x4{};
+  const int tl = 4 * grp + r16 / 4;
+  uint32_t vt_off[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) {
+    const int dt = dt0 + d;
+    vt_off[d] = tl * 256 + 8 * (lane % 2) + 16 * (((2 * dt + (lane % 4) / 2) ^ (2 * (tl % 8))));
+  }
+  prefill::block_sync();  // the first tile is in slot 0
+
+  for (int s = 0; s < steps; ++s) {
+    if (!idle) {
+      const int jt = residue + kResidues * s;
+      const bool tile_ok = tile_src(jt).ok;
+      const uint8_t* kt_lds = slot_k(s) + 16 * lane;
+      const uint8_t* vbuf = slot_v(s);
+      bf16x8 kr[2][4];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kr[kt][ks] = *(const bf16x8*)(kt_lds + 1024 * (4 * kt + ks));
+      const int t0 = jt * kTile;
+      f32x4 sc[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        f32x4 acc = f32x4{};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc = mfma16(kr[kt][ks], qv[ks], acc);
+        sc[kt] = acc;
+      }
+      const int tok0 = t0 + 4 * grp;
+      const int lim_e = (tile_ok ? lim : t0) - tok0;
+      float x[8];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = (e % 4) + 16 * (e / 4) < lim_e ? sc[e / 4][e % 4] * p.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, x[e]);
+      }
+      mx = quad_max(mx);
+      const float m_new = fmaxf(m, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2_fast(m - m_use);
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = exp2_fast(x[e] - m_use);
+        sum += x[e];
+      }
+      sum = quad_sum(sum);
+      l = l * alpha + sum;
+      m = m_new;
+      if (!__all(alpha == 1.f)) {
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[d] *= alpha;
+      }
+      u32x4 w;
+      w[0] = cvt_bf16x2(x[0], x[1]);
+      w[1] = cvt_bf16x2(x[2], x[3]);
+      w[2] = cvt_bf16x2(x[4], x[5]);
+      w[3] = cvt_bf16x2(x[6], x[7]);
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, w);
+#pragma unroll
+      for (int d = 0; d < DT; ++d) {
+        const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[d]));
+        const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[d] + 16 * 256));
+        const short e8 __attribute__((ext_vector_type(8))) = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        o[d] = mfma16(__builtin_bit_cast(bf16x8, e8), pb, o[d]);
+      }
+    }
+    prefill::block_sync();  // this slot is free again; the next tile is in the other one
+  }
+
+  // ---- this residue's partial (this wave's rows and d range); attn_combine merges the eight ----
+  if (idle || row >= rows) return;
+  const int64_t base = (((int64_t)item * p.Hkv + h) * kResidues + residue) * p.rows_alloc + row;
+  float* po = p.part_o + base * kD + 4 * grp;
+#pragma unroll
+  for (int d = 0; d < DT; ++d) *(f32x4*)(po + 16 * (dt0 + d)) = o[d];
+  if (grp == 0 && dt0 == 0) {
+    p.part_ml[base * 2 + 0] = m;
+    p.part_ml[base * 2 + 1] = l;
+  }
+}
+
+template <int RT, bool kVarlen, bool kPaged>
+__global__ __launch_bounds__(kStreamThreads, 1) void attn_stream(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kStreamLds];
+  stream_body<RT, kVarlen, kPaged>(p, lds, blockIdx.z, rotated_head(p, blockIdx.y, blockIdx.z), blockIdx.x);
+}
+
 // A varlen call with long query runs: one launch for both work lists, so that the prefill q-blocks (MFMA
 // and latency bound) and the decode / verify items (HBM bound) share the CUs. Slot x of the dispatch order
 // takes the lists interleaved, two prefill q-blocks then one residue item (each list in its own order,
@@ -811,7 +1064,7 @@ void launch_rt(int waves, dim3 items_grid, hipStream_t s, const Params& p) {
     case 8: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 8>), grid, dim3(8 * kWave), 0, s, p); break;
     case 4: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 4>), grid, dim3(4 * kWave), 0, s, p); break;
     case 2: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 2>), grid, dim3(2 * kWave), 0, s, p); break;
-    default: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 1>), grid, dim3(kWave), 0, s, p); break;
+    default: hipLaunchKernelGGL((attn_stream<RT, kVarlen, kPaged>), grid, dim3(kStreamThreads), 0, s, p); break;
   }
 }
 
@@ -822,7 +1075,7 @@ void launch_rt_small(int waves, dim3 items_grid, hipStream_t s, const Params& p)
   switch (waves) {
     case 4: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 4>), grid, dim3(4 * kWave), 0, s, p); break;
     case 2: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 2>), grid, dim3(2 * kWave), 0, s, p); break;
-    default: hipLaunchKernelGGL((attn_fwd<RT, kVarlen, kPaged, 1>), grid, dim3(kWave), 0, s, p); break;
+    default: hipLaunchKernelGGL((attn_stream<RT, kVarlen, kPaged>), grid, dim3(kStreamThreads), 0, s, p); break;
   }
 }
 
