@@ -808,7 +808,9 @@ __global__ __launch_bounds__(256) void attn_combine(Params p) {
   const int rows = it.np * p.g;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  for (int row = wave; row < rows; row += 4) {
+  // One row per wave, four rows per workgroup along z: every row's loads are in flight at once.
+  const int row = blockIdx.z * 4 + wave;
+  if (row < rows) {
     const int64_t base0 = (((int64_t)item * p.Hkv + h) * kResidues) * p.rows_alloc + row;
     float ms[kResidues], ls[kResidues];
     float2 os[kResidues];
@@ -1176,7 +1178,8 @@ int decode_run(const char* who, bool planned, const void* q, int64_t q_token_str
   launch_fwd<false, true>(RT, waves, dim3(1, num_kv_heads, (unsigned)items), s, p);
   if ((rc = check_launch(who))) return rc;
   if (partials) {
-    hipLaunchKernelGGL((attn_combine<false>), dim3((unsigned)items, num_kv_heads), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attn_combine<false>), dim3((unsigned)items, num_kv_heads, (unsigned)(p.rows_alloc / 4)),
+                       dim3(256), 0, s, p);
     if ((rc = check_launch(who))) return rc;
   }
   return kOk;
@@ -1406,7 +1409,8 @@ int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_str
     launch_rt<kVarlenRT, true, false>(waves, grid, s, p);
   if ((rc = check_launch(who))) return rc;
   if (partials) {
-    hipLaunchKernelGGL((attn_combine<true>), dim3((unsigned)items, num_kv_heads), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attn_combine<true>), dim3((unsigned)items, num_kv_heads, (unsigned)(p.rows_alloc / 4)),
+                       dim3(256), 0, s, p);
     if ((rc = check_launch(who))) return rc;
   }
   return kOk;
