@@ -390,7 +390,7 @@ def cpu_baseline(inputs, min_seconds=10.0, max_reps=8):
     import torch
     from oracle import attention as oatt
     q, kc, vc, lens, tables = inputs
-    torch.set_num_threads(min(16, os.cpu_count() or 1))   # the GPU box grants 16 host cores per GPU
+    torch.set_num_threads(min(16, os.cpu_count() or 1))   # at most 16 host threads per GPU
     qs, ls, ts = q.cpu(), lens.cpu(), tables.cpu()
     kcs, vcs = kc.cpu(), vc.cpu()
     oatt.paged_decode_attention(qs[:2], kcs, vcs, ls[:2], ts[:2], D ** -0.5)
@@ -470,8 +470,8 @@ def main():
                     help="also run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the hot path shards by sequence or "
-              "KV head with no cross-GPU exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: the library has no multi-GPU path (the hot path shards by sequence or "
+              "KV head with no cross-GPU exchange). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
