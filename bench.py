@@ -9,6 +9,7 @@ launch that rocprofv3's FETCH_SIZE + WRITE_SIZE counters measured for this launc
 profiles/), null if that summary is absent.
 
 Also reported (same JSON line):
+* the verify attention with context lengths uniform in [1024, 8192], and at B in {1, 16} x k in {1, 4, 8};
 * the KV-cache scatter (2048 rows, 10% padding slots);
 * the fused q/k RMSNorm + RoPE + KV store over 2048 tokens, next to the reference's eager operations;
 * one draft step's inputs for 64 sequences, next to the reference's tensor operations;
@@ -139,6 +140,39 @@ def bench_verify_uniform(dev, B=64, k=4, lo=1024, hi=8192, W=33):
         res[name] = dict(us=round(t * 1e6, 2), GBs=round(nbytes / t / 1e9, 1), frac=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4))
     res["bytes"] = nbytes
     res["contexts"] = f"uniform [{lo}, {hi}], seed 0, B={B}, k={k}"
+    return res
+
+
+def bench_verify_sweep(dev, ctx_len=4096, W=33):
+    """The other batch / guess-count points of the verify workload at ctx 4096: B in {1, 16}, k in {1, 4, 8},
+    through Attention.forward's path (planned order), graph-timed over calls that each read the next of
+    enough cache copies to exceed the 256 MB last-level cache."""
+    import types
+    import torch
+    from attn_cases import paged_cache, queries
+    from nanovllm_amd.layers.attention import paged_decode_attention
+    res = {}
+    for B in (1, 16):
+        ctx = [ctx_len] * B
+        kc, vc, tables = paged_cache(dev, ctx, HKV, D, W=W, seed=0)
+        copies = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(max(1, 300 // (17 * B)))]
+        lens = torch.tensor(ctx, dtype=torch.int32, device=dev)
+        for k in (1, 4, 8):
+            n = k + 1
+            q = queries(dev, B * n, HQ, D, seed=1).view(B, n, HQ, D)
+            out = torch.empty(B * n, HQ, D, dtype=torch.bfloat16, device=dev)
+            owner, turn = types.SimpleNamespace(), [0]
+
+            def call():
+                a, b = copies[turn[0] % len(copies)]
+                turn[0] += 1
+                paged_decode_attention(q, a, b, lens, tables, D ** -0.5, out=out, plan_owner=owner)
+            t = graph_timed(call, reps=len(copies))
+            nbytes = decode_bytes(ctx, n)
+            res[f"B{B}_k{k}"] = dict(us=round(t * 1e6, 2), frac=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4))
+        del kc, vc, tables, copies
+        torch.cuda.empty_cache()
+    res["contexts"] = f"{ctx_len} for every sequence"
     return res
 
 
@@ -514,6 +548,7 @@ def main():
     }
     if not args.skip_extras:
         result["verify_attention_uniform_ctx"] = bench_verify_uniform(dev)
+        result["verify_attention_sweep"] = bench_verify_sweep(dev)
         result["kv_store"] = bench_store(dev, args.steps, args.warmup)
         result["qk_norm_rope_store"] = bench_qk_norm_rope(dev)
         result["draft_step_inputs"] = bench_draft_inputs(dev)
