@@ -308,9 +308,10 @@ def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
 
 def bench_mixed_attention(dev, steps, warmup, layers=36):
     """Attention phase of a 2048-token-budget mixed step (48 verify requests with k = 4 and 3 prefill chunks,
-    config-5 lengths, Qwen3-8B shapes): per layer, store this step's KV then varlen paged attention, for 36
+    lognormal lengths, Qwen3-8B shapes): per layer, store this step's KV then varlen paged attention, for 36
     layers. Timed as one HIP-graph replay per step through the mixed-step runtime (plan + 36 x (store +
-    attention), metadata refreshed by one host-to-device copy per step), and as eager per-layer calls."""
+    attention), metadata refreshed by one host-to-device copy per step), as eager per-layer calls, and as the
+    runtime's step with each layer's q/k RMSNorm + RoPE + KV store fused in front of the attention."""
     import numpy as np
     import torch
     from types import SimpleNamespace
@@ -349,6 +350,20 @@ def bench_mixed_attention(dev, steps, warmup, layers=36):
 
     _, eager_ev = timed(eager_step, steps, warmup)
     t_eager = sum(eager_ev) / len(eager_ev)
+
+    # the same step with each layer's q/k RMSNorm + RoPE + KV store fused in front of its attention (the
+    # runner's pre_attn: qkv rows in, per-layer norm weights, Qwen3-8B rope base 1e6)
+    from nanovllm_amd.layers.rotary_embedding import RotaryEmbedding
+    g = torch.Generator(device=dev).manual_seed(9)
+    weights = [tuple((1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(torch.bfloat16) for _ in range(2))
+               for _ in range(layers)]
+    rope = RotaryEmbedding(D, D, 40960, 1e6).to(dev)
+    fused = MixedStepRunner([SimpleNamespace(k_cache=a, v_cache=b) for a, b in caches], HQ, HKV, D, D ** -0.5,
+                            block_size=BLOCK, max_num_batched_tokens=2048, max_num_seqs=64, table_width=W,
+                            pre_attn=(rope.cos_sin_cache, weights, 1e-6))
+    fused.bufs["qkv"][:N] = queries(dev, N, HQ + 2 * HKV, D, seed=9).view(N, -1)
+    _, fused_ev = timed(lambda: fused.run(layout), steps, warmup)
+    t_fused = sum(fused_ev) / len(fused_ev)
     flops = sum(4 * HQ * D * (a * (b - a) + a * (a + 1) / 2) for a, b in zip(lq[nd:], lk[nd:]))
     dec_bytes = decode_bytes(lk[:nd], 5)
     # One layer's attention kernel (work lists planned beforehand), whole step and its prefill chunks alone,
@@ -358,6 +373,7 @@ def bench_mixed_attention(dev, steps, warmup, layers=36):
     prefill_s = planned_varlen_time(q[pre], caches, lq[nd:], lk[nd:], tables[nd:].contiguous())
     return dict(ms=round(t * 1e3, 4), tok_s=round(Nq / t, 1), timing="one HIP-graph replay per step",
                 eager_ms=round(t_eager * 1e3, 4), eager_tok_s=round(Nq / t_eager, 1),
+                with_qk_norm_rope_ms=round(t_fused * 1e3, 4), with_qk_norm_rope_tok_s=round(Nq / t_fused, 1),
                 query_tokens=Nq, bucket_tokens=N, bucket_seqs=layout["S"], decode_seqs=nd,
                 prefill_chunks=len(lq) - nd, prefill_flops_per_layer=flops, decode_bytes_per_layer=dec_bytes,
                 layer_attention_us=round(layer_s * 1e6, 2),

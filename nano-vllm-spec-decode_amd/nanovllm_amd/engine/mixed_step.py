@@ -1,5 +1,5 @@
 """Mixed prefill+decode steps replayed from HIP graphs: the runtime around the attention hot path on a mixed
-step (the caller side of rows a1 / a4; counterpart of the reference's mixed-step path,
+step (the caller of the KV store and the varlen attention; counterpart of the reference's mixed-step path,
 nanovllm/engine/model_runner.py:487-589 run_mixed / run_piecewise, :605-627 buckets and buffers, :646-696
 capture).
 
@@ -8,7 +8,8 @@ every attention eagerly between the replays, because flash-attn's varlen launch 
 lengths. Here the varlen kernels' launch geometry depends only on (num_seqs, total_q, max_seqlen_q), so one
 graph per (token bucket, sequence bucket) holds the whole step: the work-list plan (once per step), then per
 layer the optional model segment, the KV-cache store and the attention. A step refreshes the metadata with one
-host-to-device copy from pinned memory and replays that graph.
+host-to-device copy from pinned memory and replays that graph. Optionally each layer's q/k RMSNorm, rotary
+embedding and KV store run fused in front of its attention (pre_attn).
 
 Padding. A step of n tokens in S_real requests runs in bucket (N, S): N >= n tokens, S >= S_real + 1
 sequences. Rows n..N-1 form one padding sequence with no keys (Lk = 0): the kernels write zeros for them and
@@ -22,6 +23,7 @@ import torch
 
 from nanovllm_amd import _lib
 from nanovllm_amd.engine.metadata import mixed_batch
+from nanovllm_amd.layers.rotary_embedding import qk_norm_rope_store
 
 
 def token_buckets(max_num_batched_tokens: int, step: int = 64) -> list[int]:
@@ -52,13 +54,15 @@ def mixed_step_layout(seqs, k: int, block_size: int, table_width: int, tok_bucke
     """Host layout of a mixed step (decode requests first, then prefill chunks, as the reference orders them,
     model_runner.py:512), padded to its bucket: the mixed_batch fields plus n (real tokens), N / S (bucket
     tokens / sequences) and `meta`, the int32 metadata in staging order: cu_seqlens_q [S+1], cu_seqlens_k
-    [S+1], slot_mapping [N], block_tables [S, table_width] (-1 padded)."""
+    [S+1], slot_mapping [N], block_tables [S, table_width] (-1 padded); `positions_padded` lists the N rows'
+    positions (0 for padding rows)."""
     b = mixed_batch(seqs, k, block_size)
     n, Sr = len(b["input_ids"]), len(seqs)
     N, S = _bucket(tok_buckets, n), _bucket(sq_buckets, Sr + 1)
     for seq in seqs:
         if len(seq.block_table) > table_width:
             raise ValueError(f"block table of {len(seq.block_table)} blocks exceeds the width {table_width}")
+    positions = list(b["positions"]) + [0] * (N - n)
     cu_q = list(b["cu_seqlens_q"]) + [N] * (S - Sr)            # sequence Sr: the padding rows n..N-1
     cu_k = list(b["cu_seqlens_k"]) + [b["cu_seqlens_k"][-1]] * (S - Sr)  # no keys
     slots = list(b["slot_mapping"]) + [-1] * (N - n)
@@ -66,7 +70,7 @@ def mixed_step_layout(seqs, k: int, block_size: int, table_width: int, tok_bucke
     for seq in seqs:
         tables += list(seq.block_table) + [-1] * (table_width - len(seq.block_table))
     tables += [-1] * ((S - Sr) * table_width)
-    b.update(n=n, N=N, S=S, meta=cu_q + cu_k + slots + tables)
+    b.update(n=n, N=N, S=S, meta=cu_q + cu_k + slots + tables, positions_padded=positions)
     return b
 
 
@@ -80,12 +84,21 @@ class MixedStepRunner:
     It must be per token (no reads of step metadata). Without it the step is attention only: bufs["q"],
     bufs["k"], bufs["v"] hold the step's rows (written by the caller) and every layer reads them.
 
+    pre_attn: optional (cos_sin_cache, norm_weights, eps): every layer's attention is preceded by the fused
+    q/k RMSNorm + rotary embedding + KV store (qk_norm_rope_store, the reference's q_norm / k_norm /
+    rotary_emb of qwen3.py:89-96 and the store of attention.py:62-63): cos_sin_cache is the RotaryEmbedding
+    buffer (fp32, [max_position, D] or [max_position, 1, D]), norm_weights a list of per-layer (q_norm, k_norm)
+    weights (None: a model with a qkv bias, no norm), eps the RMSNorm epsilon. The segments then write
+    bufs["qkv"] [N, (Hq + 2 Hkv) D] (the qkv projection's output) and the step's positions travel with its
+    metadata.
+
     Buffers (fixed addresses, sized for the largest bucket): bufs["q"] / ["o"] [N, Hq, D], bufs["k"] / ["v"]
-    [N, Hkv, D] bf16. After run(), bufs["o"][:n] is the last layer's attention output."""
+    [N, Hkv, D] bf16 (and bufs["qkv"] with pre_attn). After run(), bufs["o"][:n] is the last layer's attention
+    output."""
 
     def __init__(self, layers, num_heads: int, num_kv_heads: int, head_dim: int, scale: float,
                  block_size: int = 256, max_num_batched_tokens: int = 2048, max_num_seqs: int = 256,
-                 table_width: int = 16, token_step: int = 64, segment=None, device=None):
+                 table_width: int = 16, token_step: int = 64, segment=None, device=None, pre_attn=None):
         self.layers = list(layers)
         self.Hq, self.Hkv, self.D, self.scale = num_heads, num_kv_heads, head_dim, scale
         self.block_size, self.W = block_size, table_width
@@ -101,6 +114,16 @@ class MixedStepRunner:
             v=torch.zeros(Nmax, num_kv_heads, head_dim, dtype=torch.bfloat16, device=dev),
             o=torch.zeros(Nmax, num_heads, head_dim, dtype=torch.bfloat16, device=dev),
         )
+        self.pre_attn = None
+        if pre_attn is not None:
+            cos_sin, weights, eps = pre_attn
+            if weights is not None and len(weights) != len(self.layers):
+                raise ValueError("pre_attn: one (q_norm, k_norm) pair per layer")
+            self.pre_attn = (cos_sin.reshape(cos_sin.size(0), -1), weights, float(eps))
+            self.bufs["qkv"] = torch.zeros(Nmax, (num_heads + 2 * num_kv_heads) * head_dim, dtype=torch.bfloat16,
+                                           device=dev)
+            self._pos = torch.zeros(Nmax, dtype=torch.int64, device=dev)
+            self._pos_staging = torch.zeros(Nmax, dtype=torch.int64, pin_memory=True)
         meta_len = 2 * (Smax + 1) + Nmax + Smax * table_width
         self._meta = torch.zeros(meta_len, dtype=torch.int32, device=dev)
         self._staging = torch.zeros(meta_len, dtype=torch.int32, pin_memory=True)
@@ -128,9 +151,13 @@ class MixedStepRunner:
     def load(self, layout: dict) -> None:
         """Copies a prepared layout's metadata to the bucket's device views (one copy, current stream)."""
         meta = layout["meta"]
-        self._copied.synchronize()  # the previous step's copy may still read the staging buffer
+        self._copied.synchronize()  # the previous step's copies may still read the staging buffers
         self._staging[:len(meta)] = torch.tensor(meta, dtype=torch.int32)
         self._meta[:len(meta)].copy_(self._staging[:len(meta)], non_blocking=True)
+        if self.pre_attn is not None:
+            pos = layout["positions_padded"]
+            self._pos_staging[:len(pos)] = torch.tensor(pos, dtype=torch.int64)
+            self._pos[:len(pos)].copy_(self._pos_staging[:len(pos)], non_blocking=True)
         self._copied.record(torch.cuda.current_stream(self.device))
 
     # ---- device side ----
@@ -148,9 +175,17 @@ class MixedStepRunner:
             if self.segment is not None:
                 self.segment(i, N, self.bufs)
             kc, vc = layer.k_cache, layer.v_cache
-            _lib.check(lib.sd_store_kvcache(k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), kc.data_ptr(),
-                                            vc.data_ptr(), kc.numel() // (Hkv * D), slots.data_ptr(), N, Hkv, D,
-                                            stream), "sd_store_kvcache")
+            if self.pre_attn is not None:
+                cos_sin, weights, eps = self.pre_attn
+                qkv = self.bufs["qkv"][:N]
+                qw, kw = weights[i] if weights is not None else (None, None)
+                qk_norm_rope_store(self._pos[:N], qkv[:, :Hq * D].view(N, Hq, D),
+                                   qkv[:, Hq * D:(Hq + Hkv) * D].view(N, Hkv, D), qkv[:, (Hq + Hkv) * D:].view(N, Hkv, D),
+                                   qw, kw, eps, cos_sin, kc, vc, slots, q_out=q[:N], write_k=False)
+            else:
+                _lib.check(lib.sd_store_kvcache(k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), kc.data_ptr(),
+                                                vc.data_ptr(), kc.numel() // (Hkv * D), slots.data_ptr(), N, Hkv, D,
+                                                stream), "sd_store_kvcache")
             _lib.check(lib.sd_varlen_attention_planned(
                 q.data_ptr(), q.stride(0), kc.data_ptr(), Hkv * D, vc.data_ptr(), Hkv * D, 0, kc.size(0), bs,
                 tables.data_ptr(), W, cu_q.data_ptr(), cu_k.data_ptr(), S, N, N, W * bs, Hq, Hkv, D, self.scale,

@@ -110,3 +110,52 @@ def test_mixed_step_eager_body_matches_graph(device):
     replay = runner.run(layout).clone()       # replays it
     torch.cuda.synchronize()
     assert torch.equal(eager, first) and torch.equal(eager, replay)
+
+
+def test_mixed_step_with_fused_pre_attention(device):
+    """pre_attn: every layer's q/k RMSNorm + rotary embedding + KV store run fused in the step's graph. Two
+    steps in one bucket (the second a replay) give bitwise the outputs and caches of eager per-layer calls:
+    qk_norm_rope_store on the unpadded rows, then the varlen attention."""
+    from nanovllm_amd.layers.rotary_embedding import qk_norm_rope_store
+    from oracle import qk_norm_rope as onr
+    lq, lk = mixed_step(1)
+    nd = 48
+    W = math.ceil(max(lk) / BLOCK)
+    kc, vc, tables = paged_cache(device, lk, HKV, D, W=W, seed=7)
+    graph_caches = [(kc.clone(), vc.clone()) for _ in range(LAYERS)]
+    eager_caches = [(kc.clone(), vc.clone()) for _ in range(LAYERS)]
+    del kc, vc
+    g = torch.Generator().manual_seed(8)
+    weights = [tuple((1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16).to(device) for _ in range(2))
+               for _ in range(LAYERS)]
+    cs = onr.rope_cache(D, 16384, 1e6).to(device)
+    layers = [SimpleNamespace(k_cache=a, v_cache=b) for a, b in graph_caches]
+    runner = MixedStepRunner(layers, HQ, HKV, D, D ** -0.5, block_size=BLOCK, max_num_seqs=64, table_width=W,
+                             pre_attn=(cs, weights, 1e-6))
+    tb = tables.cpu()
+    for i in range(2):
+        layout = runner.prepare(_requests(lq, lk, tb, nd), K)
+        n, N, S = layout["n"], layout["N"], layout["S"]
+        qkv = queries(device, N, HQ + 2 * HKV, D, seed=50 + i).view(N, -1)
+        runner.bufs["qkv"][:N] = qkv
+        out = runner.run(layout).clone()
+        # eager reference on the unpadded rows
+        pos = torch.tensor(layout["positions"], dtype=torch.int64, device=device)
+        slots = torch.tensor(layout["slot_mapping"], dtype=torch.int32, device=device)
+        cu_q = torch.tensor(layout["cu_seqlens_q"], dtype=torch.int32, device=device)
+        cu_k = torch.tensor(layout["cu_seqlens_k"], dtype=torch.int32, device=device)
+        Sr = len(layout["cu_seqlens_q"]) - 1
+        tab = torch.tensor(layout["meta"][2 * (S + 1) + N:], dtype=torch.int32, device=device).view(S, W)[:Sr]
+        x = qkv[:n]
+        ref = None
+        for (ek, ev), (qw, kw) in zip(eager_caches, weights):
+            q, _ = qk_norm_rope_store(pos, x[:, :HQ * D].view(n, HQ, D), x[:, HQ * D:(HQ + HKV) * D].view(n, HKV, D),
+                                      x[:, (HQ + HKV) * D:].view(n, HKV, D), qw, kw, 1e-6, cs, ek, ev, slots,
+                                      write_k=False)
+            ref = varlen_attention(q, ek, ev, cu_q, cu_k, layout["max_seqlen_q"], layout["max_seqlen_k"], D ** -0.5,
+                                   tab.contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"step {i}: fused pre-attention step differs from the eager calls"
+        for l, ((gk, gv), (ek, ev)) in enumerate(zip(graph_caches, eager_caches)):
+            assert torch.equal(gk, ek) and torch.equal(gv, ev), f"step {i} layer {l}: caches differ"
+    assert len(runner.graphs) == 1
