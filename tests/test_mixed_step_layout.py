@@ -41,6 +41,7 @@ def test_padded_layout_known_answer():
     assert slots == [3 * BS + 1, 3 * BS + 2, 3 * BS + 3, 0, 1, 2, 3, 4, 5] + [-1] * 7
     assert tables == [7, 3, -1, -1, 0, 1, 2, -1] + [-1] * 8
     assert len(meta) == 2 * (S + 1) + N + S * W
+    assert b["positions_padded"] == [5, 6, 7, 0, 1, 2, 3, 4, 5] + [0] * 7   # padding rows at position 0
 
 
 def test_layout_limits():
