@@ -459,11 +459,18 @@ def cpu_baseline(inputs, min_seconds=10.0, max_reps=8):
 
 
 def cpu_secondary(reps=3):
-    """The oracle on the secondary workloads' shapes (same threads): the fused q/k norm + RoPE + store over 2048
-    tokens and one draft step's inputs for 64 sequences; milliseconds per call, best of `reps`."""
+    """The oracle on the secondary workloads' shapes (same threads), milliseconds per call: the KV scatter of
+    2048 rows, the fused q/k norm + RoPE + store over 2048 tokens and one draft step's inputs for 64 sequences
+    (best of `reps`); the verifier at S 64, K 4, V 151936 (T 0, and T 1 with draft logits) and one layer of
+    the mixed step's attention (one run each)."""
+    import numpy as np
     import torch
+    from oracle import attention as oatt
     from oracle import draft_inputs as odi
+    from oracle import kvcache as okv
     from oracle import qk_norm_rope as onr
+    from oracle import sampler as osmp
+    from test_gpu_varlen import mixed_step
     g = torch.Generator().manual_seed(7)
     N, NB, W = 2048, 512, 33
     qkv = torch.randn(N, (HQ + 2 * HKV) * D, generator=g).to(torch.bfloat16)
@@ -481,17 +488,44 @@ def cpu_secondary(reps=3):
     tables = torch.randperm(4096, generator=g)[:64 * W].view(64, W).to(torch.int32)
     toks = torch.randint(0, 151936, (64,), generator=g)
     out = {}
-    for name, fn in (("qk_norm_rope_store_2048_tokens_ms",
-                      lambda: onr.qk_norm_rope_store(q, k, v, pos, w, w, 1e-6, cs, kc, vc, slots)),
-                     ("draft_step_inputs_64_seqs_ms",
-                      lambda: odi.draft_step_inputs(real, last, tables, BLOCK, toks, 1))):
+
+    def clock(name, fn, n):
         best = float("inf")
-        for _ in range(reps):
+        for _ in range(n):
             t0 = time.perf_counter()
             fn()
             best = min(best, time.perf_counter() - t0)
         out[name] = round(best * 1e3, 3)
-    del kc, vc
+
+    clock("kv_store_2048_rows_ms", lambda: okv.store_kvcache(k, v, kc, vc, slots), reps)
+    clock("qk_norm_rope_store_2048_tokens_ms",
+          lambda: onr.qk_norm_rope_store(q, k, v, pos, w, w, 1e-6, cs, kc, vc, slots), reps)
+    clock("draft_step_inputs_64_seqs_ms", lambda: odi.draft_step_inputs(real, last, tables, BLOCK, toks, 1), reps)
+    del kc, vc, qkv, q, k, v
+    S, K, V = 64, 4, 151936
+    logits = torch.randn(S * (K + 1), V, generator=g) * 3
+    dlog = torch.randn(S, K, V, generator=g) * 3
+    drafts, nd = dlog.argmax(-1), torch.full((S,), K)
+    u, e = torch.rand(S, K, generator=g), torch.empty(S, V).exponential_(1, generator=g)
+    for T in (0.0, 1.0):
+        clock(f"verify_T{int(T)}_ms", lambda: osmp.verify_drafts(logits, drafts, nd, torch.full((S,), T),
+                                                                 dlog if T else None, uniforms=u, exp_noise=e), 1)
+    del logits, dlog, e
+    lq, lk = mixed_step(0)
+    Wm = math.ceil(max(lk) / BLOCK)
+    nblk = sum(math.ceil(c / BLOCK) for c in lk)
+    kcm = torch.randn(nblk, BLOCK, HKV, D, generator=g).to(torch.bfloat16)
+    vcm = torch.randn(nblk, BLOCK, HKV, D, generator=g).to(torch.bfloat16)
+    tab = torch.full((len(lk), Wm), -1, dtype=torch.int32)
+    b = 0
+    for i, c in enumerate(lk):
+        nb = math.ceil(c / BLOCK)
+        tab[i, :nb] = torch.arange(b, b + nb)
+        b += nb
+    qm = torch.randn(sum(lq), HQ, D, generator=g).to(torch.bfloat16)
+    cu_q = torch.tensor([0] + np.cumsum(lq).tolist(), dtype=torch.int32)
+    cu_k = torch.tensor([0] + np.cumsum(lk).tolist(), dtype=torch.int32)
+    clock("mixed_step_attention_one_layer_ms", lambda: oatt.varlen_attention(qm, kcm, vcm, cu_q, cu_k, D ** -0.5, tab), 1)
     return out
 
 
