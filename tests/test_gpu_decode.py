@@ -113,10 +113,11 @@ def test_repeatable_bitwise(device):
     assert torch.equal(a, b)
 
 
-def test_graph_capture_at_zero_lengths_then_replay(device):
+@pytest.mark.parametrize("B", [16, 2])   # 2: the streaming kernel for few (sequence, head) pairs
+def test_graph_capture_at_zero_lengths_then_replay(device, B):
     """Captured like capture_cudagraph (all context_lens 0, zero block tables), replayed with real metadata
     copied into the same buffers; every replay equals the eager result bitwise."""
-    Hq, Hkv, D, W, n, B = 32, 8, 128, 33, 5, 16
+    Hq, Hkv, D, W, n = 32, 8, 128, 33, 5
     rnd = random.Random(5)
     ctx_all = [[rnd.randint(1024, 8192) for _ in range(B)] for _ in range(3)]
     kc, vc, _ = paged_cache(device, [8192] * B, Hkv, D, W=W, seed=31, extra_blocks=64)
