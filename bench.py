@@ -14,6 +14,7 @@ Also reported (same JSON line):
 * the fused q/k RMSNorm + RoPE + KV store over 2048 tokens, next to the reference's eager operations;
 * one draft step's inputs for 64 sequences, next to the reference's tensor operations;
 * the rejection sampler (S 64, K 4, V 151936, T 0 and T 1 with draft logits);
+* the unfused path in front of it: the LM head as the library GEMM into bf16 logits, then the T 0 verifier;
 * a 2048-token mixed prefill+decode attention step over 36 layers, replayed as one HIP graph by the mixed-step
   runtime (tok/s), and the prefill kernel at GPU-filling sizes;
 * a CPU baseline: the oracle (PyTorch CPU restatement) timed on the headline workload for about 10 s on 16
@@ -306,6 +307,40 @@ def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
     return res
 
 
+def bench_lm_head_verify(dev, S=64, K=4, V=151936, H=4096):
+    """The unfused path in front of the verifier: the LM head as the library GEMM (F.linear, as
+    embed_head.py:63 computes it) over the S(K+1) verify rows into bf16 logits, then sd_verify_drafts at
+    T = 0 on them. Reports each part and what fusing the verify statistics into the GEMM could save at most:
+    the logits' write and re-read at the HBM rate the verifier reaches."""
+    import torch
+    import torch.nn.functional as F
+    from nanovllm_amd.layers.sampler import verify_drafts
+    g = torch.Generator(device=dev).manual_seed(9)
+    h = (torch.randn(S * (K + 1), H, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    w = (torch.randn(V, H, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    logits = torch.empty(S * (K + 1), V, device=dev, dtype=torch.bfloat16)
+    drafts = torch.randint(0, V, (S, K), device=dev, generator=g)
+    nd = torch.full((S,), K, device=dev)
+    temps = torch.zeros(S, device=dev)
+    u = torch.rand(S, K, device=dev, generator=g)
+    e = torch.empty(S, V, device=dev).exponential_(1, generator=g)
+    t_gemm = graph_timed(lambda: F.linear(h, w), reps=5)
+    logits.copy_(F.linear(h, w))
+    t_verify = graph_timed(lambda: verify_drafts(logits, drafts, nd, temps, None, uniforms=u, exp_noise=e), reps=10)
+    t_both = graph_timed(lambda: verify_drafts(F.linear(h, w), drafts, nd, temps, None, uniforms=u, exp_noise=e),
+                         reps=5)
+    flops = 2.0 * S * (K + 1) * H * V
+    w_bytes = V * H * 2
+    logit_bytes = S * (K + 1) * V * 2
+    verify_rate = logit_bytes / t_verify
+    return dict(
+        shape=f"[{S * (K + 1)}, {H}] x [{H}, {V}] bf16",
+        gemm_us=t_gemm * 1e6, gemm_tflops=flops / t_gemm / 1e12, gemm_mfma_frac=flops / t_gemm / 2.5e15,
+        gemm_weight_TBs=w_bytes / t_gemm / 1e12, verify_us=t_verify * 1e6, gemm_then_verify_us=t_both * 1e6,
+        fusion_saving_bound_us=2 * logit_bytes / verify_rate * 1e6,
+        timing="graph replays; logits bf16 as the engine's LM head writes them")
+
+
 def bench_mixed_attention(dev, steps, warmup, layers=36):
     """Attention phase of a 2048-token-budget mixed step (48 verify requests with k = 4 and 3 prefill chunks,
     lognormal lengths, Qwen3-8B shapes): per layer, store this step's KV then varlen paged attention, for 36
@@ -548,7 +583,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-extras", action="store_true", help="headline only (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="leave out the CPU baseline (for profiling)")
-    ap.add_argument("--only", choices=["qk_norm_rope_store", "draft_step_inputs", "kv_store"],
+    ap.add_argument("--only", choices=["qk_norm_rope_store", "draft_step_inputs", "kv_store", "lm_head_verify"],
                     help="run one secondary workload alone and print its JSON (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
@@ -568,7 +603,8 @@ def main():
         del src, dst
     if args.only:
         fn = {"qk_norm_rope_store": lambda: bench_qk_norm_rope(dev), "draft_step_inputs": lambda: bench_draft_inputs(dev),
-              "kv_store": lambda: bench_store(dev, args.steps, args.warmup)}[args.only]
+              "kv_store": lambda: bench_store(dev, args.steps, args.warmup),
+              "lm_head_verify": lambda: bench_lm_head_verify(dev)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
     head = bench_verify_attention(dev, args.steps, args.warmup)
@@ -603,6 +639,7 @@ def main():
         result["qk_norm_rope_store"] = bench_qk_norm_rope(dev)
         result["draft_step_inputs"] = bench_draft_inputs(dev)
         result["verify_sampler"] = bench_sampler(dev, max(10, args.steps // 2), args.warmup)
+        result["lm_head_then_verify"] = bench_lm_head_verify(dev)
         mixed = bench_mixed_attention(dev, max(5, args.steps // 10), 2)
         result["mixed_step_attention"] = mixed
         result["prefill_kernel"] = bench_prefill(dev)
