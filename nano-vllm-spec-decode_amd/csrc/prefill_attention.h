@@ -3,14 +3,16 @@
 // at most kResidueMaxQ queries stay on the residue kernel of paged_attention.hip).
 //
 // Prefill is MFMA work (Q·K^T and P·V over many query rows per key), so the decomposition differs from the
-// HBM-streaming decode kernel: one 8-wave workgroup owns a q-block of 128 rows (P query positions x g query
-// heads of one KV head) and walks the keys in 32-key tiles shared through LDS by all its waves.
-//   * wave w: row group rg = w % 4 (rows 32rg .. 32rg+31 of the block), parity w / 4: it takes the tiles
-//     t with t % 2 == parity, with its own online softmax; the two parity partials are merged at the end
-//     (parity 0 then 1, fixed order). The reduction therefore depends only on key positions and a row's
-//     result is the same whichever chunk, q-block or batch the row is computed in.
-//   * A stage is one K and one V tile per parity (32 KB). Each lane loads 4 x 16 B of it into registers
-//     two stages ahead and writes them to the LDS double buffer one stage ahead; one barrier per stage.
+// HBM-streaming decode kernel: one 8-wave workgroup owns a q-block of 128 or 256 rows (P query positions x g
+// query heads of one KV head) and walks the keys in 32-key tiles shared through LDS by all its waves.
+//   * 128 rows: wave w is row group rg = w % 4 (rows 32rg .. 32rg+31 of the block) of parity w / 4: it takes
+//     the tiles t with t % 2 == parity, with its own online softmax; the two parity partials are merged at
+//     the end (parity 0 then 1, fixed order). 256 rows: wave w is row group w and takes every tile.
+//     Either way the reduction depends only on key positions, and a row's result is the same whichever
+//     chunk, q-block or batch the row is computed in (for a given q-block size).
+//   * A stage is one K and one V tile per parity (32 KB with two parities, 16 KB with one). Each lane loads
+//     its 16-byte pieces of it (4 or 2) into registers two stages ahead and writes them to the LDS double
+//     buffer one stage ahead; one barrier per stage.
 //     Register staging (rather than global_load_lds) keeps every wait count visible to the compiler.
 //   * v_mfma_f32_32x32x16_bf16 for both products:
 //       S^T[32 keys x 32 rows] = K . Q^T   A = K from LDS (ds_read_b128), B = Q in registers
@@ -32,8 +34,10 @@ namespace sd {
 // Sequences with at most this many queries in a varlen call take the residue kernel (the decode / verify
 // arithmetic, bitwise equal to sd_paged_decode); longer query runs take the prefill kernel.
 constexpr int kResidueMaxQ = 16;
-// Rows (query position x query head of one KV head) per prefill workgroup.
-constexpr int kPrefillRows = 128;
+// Rows (query position x query head of one KV head) per prefill q-block: 128 (the 8 waves as 4 row groups x
+// 2 parities) or 256 (8 row groups, one parity).
+constexpr int kPrefillRowsSmall = 128;
+constexpr int kPrefillRowsLarge = 256;
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -53,7 +57,7 @@ struct PrefillArgs {
   int32_t max_items;            // grid size (upper bound of *work_count)
   int32_t total_q;
   int64_t total_k;
-  int32_t Hkv, g, P;            // P = query positions per q-block (P * g <= kPrefillRows)
+  int32_t Hkv, g, P;            // P = query positions per q-block (P * g <= the q-block's rows)
   float scale_log2;             // softmax scale * log2(e)
   uint16_t* out;
   int64_t out_stride;
@@ -66,22 +70,17 @@ namespace prefill {
 
 constexpr int kD = 128;
 constexpr int kTile = 32;                              // keys per tile
-constexpr int kRowGroups = 4;                          // waves per parity
-constexpr int kParities = 2;
-constexpr int kWaves = kRowGroups * kParities;         // 8
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;               // 512
 constexpr int kTileBytes = kTile * kD * 2;             // one K or V tile: 8 KB
-constexpr int kStageBytes = kParities * 2 * kTileBytes;  // [parity][K, V]: 32 KB
+constexpr int kStageBytesMax = 2 * 2 * kTileBytes;     // [parity][K, V] with two parities: 32 KB
 constexpr int kStages = 2;                             // LDS stage buffers
 constexpr int kMaxBlocks = 1024;                       // block-table entries staged in LDS
 constexpr float kLazyLog2 = 8.f;                       // rescale threshold (exp2 domain)
-constexpr int kLoadsPerWave = kStageBytes / (kWaves * kWave * 16);  // 16-byte loads per lane per stage
-constexpr int kLdsBytes = kStages * kStageBytes + kMaxBlocks * 4 + kWaves * 4;  // + per-wave flags
-static_assert(kLoadsPerWave == 4, "stage loads: 8 waves x 4 x 1 KB");
-static_assert(kRowGroups * 32 == kPrefillRows, "q-block rows");
-// The parity merge reuses the stage buffers and the block ids: O of the four parity-1 waves (64 fp32 per
-// lane) + (m, l).
-static_assert(kRowGroups * 64 * kWave * 4 + kRowGroups * 2 * kWave * 4 <= kLdsBytes, "merge area");
+constexpr int kLdsBytes = kStages * kStageBytesMax + kMaxBlocks * 4 + kWaves * 4;  // + per-wave flags
+// The parity merge (two parities, four row groups) reuses the stage buffers and the block ids: O of the four
+// parity-1 waves (64 fp32 per lane) + (m, l).
+static_assert(4 * 64 * kWave * 4 + 4 * 2 * kWave * 4 <= kLdsBytes, "merge area");
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -100,9 +99,15 @@ __device__ __forceinline__ void block_sync() {
   asm volatile("" ::: "memory");
 }
 
-// One q-block (work item `widx`, KV head h) with the workgroup's 512 threads; `lds` holds kLdsBytes.
-template <bool kPaged>
+// One q-block (work item `widx`, KV head h) of kRowGroups * 32 rows with the workgroup's 512 threads; `lds`
+// holds kLdsBytes. kRowGroups = 4: two parities; kRowGroups = 8: one parity, every wave takes every tile.
+template <bool kPaged, int kRowGroups>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds, int widx, int h) {
+  static_assert(kRowGroups == 4 || kRowGroups == 8, "q-blocks of 128 or 256 rows");
+  constexpr int kParities = kWaves / kRowGroups;
+  constexpr int kStageBytes = kParities * 2 * kTileBytes;              // [parity][K, V]
+  constexpr int kLoadsPerWave = kStageBytes / (kWaves * kWave * 16);  // 16-byte loads per lane per stage
+  static_assert(kStageBytes <= kStageBytesMax && kLoadsPerWave * kWaves * 1024 == kStageBytes, "stage loads");
   if (widx >= *p.work_count) return;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -132,7 +137,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
 
   // ---- block ids of the keys the block sees (to LDS below) and this lane's row: Q (B operand of S^T:
   // d = 16s + 8*half + e) and its visible-key limit; both loads in flight together ----
-  int32_t* blk_ids = (int32_t*)(lds + kStages * kStageBytes);
+  int32_t* blk_ids = (int32_t*)(lds + kStages * kStageBytesMax);
   const int nblk_row = min(p.table_width, kMaxBlocks);
   const int nb_used = kPaged ? min((kmax + p.block_size - 1) / p.block_size, nblk_row) : 0;
   int32_t blk_pre[2];
@@ -193,13 +198,15 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   // The block id of tile t as read from LDS (0 past the last tile); read a step before it is needed, so
   // that the read completes under that step's compute.
   auto tile_block_raw = [&](int t) { return (!kPaged || t >= ntiles) ? 0 : blk_ids[tile_index(t)]; };
-  // Wave w loads the tile of parity w / 4, K (w / 2 even) or V, 1 KB slots 4*(w%2) .. +3 of it: lane L of
-  // slot j writes LDS bytes 16L.. of the slot, i.e. key 4j + L/16, physical chunk L%16, so it fetches the
-  // logical chunk that the swizzle stores there. Stages past the last tile load valid rows that are never
-  // stored, so that every stage issues the same loads (static wait counts).
-  const int ld_par = wave / 4;
-  const bool ld_v = (wave / 2) % 2;
-  const int ld_slot0 = 4 * (wave % 2);
+  // The kRowGroups waves of a parity load its K and V tiles (16 slots of 1 KB): wave w loads parity
+  // w / kRowGroups, K in the first half of those waves and V in the second, kLoadsPerWave consecutive slots
+  // each (two parities: slots 4*(w%2) .. +3; one parity: slots 2*(w%4) .. +1). Lane L of slot j writes LDS
+  // bytes 16L.. of the slot, i.e. key 4j + L/16, physical chunk L%16, so it fetches the logical chunk that
+  // the swizzle stores there. Stages past the last tile load valid rows that are never stored, so that every
+  // stage issues the same loads (static wait counts).
+  const int ld_par = wave / kRowGroups;
+  const bool ld_v = (wave % kRowGroups) >= kRowGroups / 2;
+  const int ld_slot0 = kLoadsPerWave * (wave % (kRowGroups / 2));
   const uint8_t* ld_src = (const uint8_t*)(ld_v ? p.v : p.k) + h * kD * 2;
   const int64_t ld_stride = ld_v ? vsb : ksb;
   uint32_t ld_off[kLoadsPerWave];   // byte offset of this lane's chunk inside key row `key`
@@ -374,30 +381,36 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
     block_sync();
   }
 
-  // ---- merge the two parities (parity 0 then 1) and write bf16 rows ----
+  // ---- merge the two parities (parity 0 then 1) and write bf16 rows; one parity: normalize only ----
   uint32_t la = __builtin_bit_cast(uint32_t, l_part), lb = la;
   swap32(la, lb);
   const float l_row = __builtin_bit_cast(float, la) + __builtin_bit_cast(float, lb);
-  block_sync();  // every wave is done with the stage buffers
   float* mo = (float*)lds;                                    // [rg][64 values][64 lanes]
-  float* mml = (float*)(lds + kRowGroups * 64 * kWave * 4);   // [rg][m, l][64 lanes]
-  if (par == 1) {
+  float* mml = (float*)(lds + 4 * 64 * kWave * 4);            // [rg][m, l][64 lanes]
+  float f0 = 1.f, f1 = 0.f, L = l_row;
+  if constexpr (kParities == 2) {
+    block_sync();  // every wave is done with the stage buffers
+    if (par == 1) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mo[(rg * 64 + dt * 16 + r) * kWave + lane] = o[dt][r];
-    mml[(rg * 2 + 0) * kWave + lane] = m_run;
-    mml[(rg * 2 + 1) * kWave + lane] = l_row;
+        for (int r = 0; r < 16; ++r) mo[(rg * 64 + dt * 16 + r) * kWave + lane] = o[dt][r];
+      mml[(rg * 2 + 0) * kWave + lane] = m_run;
+      mml[(rg * 2 + 1) * kWave + lane] = l_row;
+    }
+    block_sync();
   }
-  block_sync();
   wait_vm_all();  // the last two (unused) stage loads
   if (par == 1 || row >= rows) return;
-  const float m1 = mml[(rg * 2 + 0) * kWave + lane];
-  const float l1 = mml[(rg * 2 + 1) * kWave + lane];
-  const float M = fmaxf(m_run, m1);
-  const float Mu = M == -INFINITY ? 0.f : M;
-  const float f0 = exp2_fast((m_run - Mu) * sl2), f1 = exp2_fast((m1 - Mu) * sl2);
-  const float L = __builtin_fmaf(l1, f1, l_row * f0);
+  if constexpr (kParities == 2) {
+    const float m1 = mml[(rg * 2 + 0) * kWave + lane];
+    const float l1 = mml[(rg * 2 + 1) * kWave + lane];
+    const float M = fmaxf(m_run, m1);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    f0 = exp2_fast((m_run - Mu) * sl2);
+    f1 = exp2_fast((m1 - Mu) * sl2);
+    L = __builtin_fmaf(l1, f1, l_row * f0);
+  }
   const float inv = L == 0.f ? 0.f : 1.f / L;
   const int i = p0 + row / p.g;
   const int hq = h * p.g + row % p.g;
@@ -410,7 +423,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 4 * j + e;
-        v4[e] = __builtin_fmaf(mo[(rg * 64 + dt * 16 + r) * kWave + lane], f1, o[dt][r] * f0) * inv;
+        if constexpr (kParities == 2)
+          v4[e] = __builtin_fmaf(mo[(rg * 64 + dt * 16 + r) * kWave + lane], f1, o[dt][r] * f0) * inv;
+        else
+          v4[e] = o[dt][r] * inv;
       }
       uint2 w;
       w.x = cvt_bf16x2(v4[0], v4[1]);
