@@ -10,9 +10,9 @@
 //     the end (parity 0 then 1, fixed order). 256 rows: wave w is row group w and takes every tile.
 //     Either way the reduction depends only on key positions, and a row's result is the same whichever
 //     chunk, q-block or batch the row is computed in (for a given q-block size).
-//   * A stage is one K and one V tile per parity (32 KB with two parities, 16 KB with one). Each lane loads
-//     its 16-byte pieces of it (4 or 2) into registers two stages ahead and writes them to the LDS double
-//     buffer one stage ahead; one barrier per stage.
+//   * A stage is one or two consecutive K and V tiles (16 or 32 KB; with two parities, one tile per parity).
+//     Each lane loads its 16-byte pieces of it (2 or 4) into registers two stages ahead and writes them to
+//     the LDS double buffer one stage ahead; one barrier per stage.
 //     Register staging (rather than global_load_lds) keeps every wait count visible to the compiler.
 //   * v_mfma_f32_32x32x16_bf16 for both products:
 //       S^T[32 keys x 32 rows] = K . Q^T   A = K from LDS (ds_read_b128), B = Q in registers
@@ -101,12 +101,16 @@ __device__ __forceinline__ void block_sync() {
 
 // One q-block (work item `widx`, KV head h) of kRowGroups * 32 rows with the workgroup's 512 threads; `lds`
 // holds kLdsBytes. kRowGroups = 4: two parities; kRowGroups = 8: one parity, every wave takes every tile.
-template <bool kPaged, int kRowGroups>
+// A stage holds kStageTiles consecutive tiles; the wave of parity `par` computes tiles par, par + kParities,
+// ... of each stage.
+template <bool kPaged, int kRowGroups, int kStageTiles>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds, int widx, int h) {
   static_assert(kRowGroups == 4 || kRowGroups == 8, "q-blocks of 128 or 256 rows");
   constexpr int kParities = kWaves / kRowGroups;
-  constexpr int kStageBytes = kParities * 2 * kTileBytes;              // [parity][K, V]
+  static_assert(kStageTiles % kParities == 0 && (kStageTiles == 1 || kStageTiles == 2), "tiles per stage");
+  constexpr int kStageBytes = kStageTiles * 2 * kTileBytes;            // [tile][K, V]
   constexpr int kLoadsPerWave = kStageBytes / (kWaves * kWave * 16);  // 16-byte loads per lane per stage
+  constexpr int kTileWaves = kWaves / kStageTiles;                     // waves loading one tile's K and V
   static_assert(kStageBytes <= kStageBytesMax && kLoadsPerWave * kWaves * 1024 == kStageBytes, "stage loads");
   if (widx >= *p.work_count) return;
   const int tid = threadIdx.x;
@@ -133,7 +137,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   const int rows = np * p.g;
   const int kmax = min(max(Lk - Lq + p0 + np, 0), Lk);  // keys seen by the block's last position
   const int ntiles = (kmax + kTile - 1) / kTile;
-  const int niter = (ntiles + kParities - 1) / kParities;
+  const int niter = (ntiles + kStageTiles - 1) / kStageTiles;
 
   // ---- block ids of the keys the block sees (to LDS below) and this lane's row: Q (B operand of S^T:
   // d = 16s + 8*half + e) and its visible-key limit; both loads in flight together ----
@@ -198,15 +202,15 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   // The block id of tile t as read from LDS (0 past the last tile); read a step before it is needed, so
   // that the read completes under that step's compute.
   auto tile_block_raw = [&](int t) { return (!kPaged || t >= ntiles) ? 0 : blk_ids[tile_index(t)]; };
-  // The kRowGroups waves of a parity load its K and V tiles (16 slots of 1 KB): wave w loads parity
-  // w / kRowGroups, K in the first half of those waves and V in the second, kLoadsPerWave consecutive slots
-  // each (two parities: slots 4*(w%2) .. +3; one parity: slots 2*(w%4) .. +1). Lane L of slot j writes LDS
-  // bytes 16L.. of the slot, i.e. key 4j + L/16, physical chunk L%16, so it fetches the logical chunk that
-  // the swizzle stores there. Stages past the last tile load valid rows that are never stored, so that every
-  // stage issues the same loads (static wait counts).
-  const int ld_par = wave / kRowGroups;
-  const bool ld_v = (wave % kRowGroups) >= kRowGroups / 2;
-  const int ld_slot0 = kLoadsPerWave * (wave % (kRowGroups / 2));
+  // kTileWaves waves load each tile of a stage (K and V: 16 slots of 1 KB): wave w loads tile
+  // w / kTileWaves of the stage, K in the first half of those waves and V in the second, kLoadsPerWave
+  // consecutive slots each (two tiles a stage: slots 4*(w%2) .. +3; one: slots 2*(w%4) .. +1). Lane L of
+  // slot j writes LDS bytes 16L.. of the slot, i.e. key 4j + L/16, physical chunk L%16, so it fetches the
+  // logical chunk that the swizzle stores there. Stages past the last tile load valid rows that are never
+  // stored, so that every stage issues the same loads (static wait counts).
+  const int ld_par = wave / kTileWaves;
+  const bool ld_v = (wave % kTileWaves) >= kTileWaves / 2;
+  const int ld_slot0 = kLoadsPerWave * (wave % (kTileWaves / 2));
   const uint8_t* ld_src = (const uint8_t*)(ld_v ? p.v : p.k) + h * kD * 2;
   const int64_t ld_stride = ld_v ? vsb : ksb;
   uint32_t ld_off[kLoadsPerWave];   // byte offset of this lane's chunk inside key row `key`
@@ -222,7 +226,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   }
   // Paged: a wave-uniform base address (the tile's first key row) plus 32-bit lane offsets.
   auto load_stage = [&](int it, int blk_raw, u32x4 (&r)[kLoadsPerWave]) {
-    const int t = kParities * it + ld_par;
+    const int t = kStageTiles * it + ld_par;
     if (kPaged) {
       const int blk = __builtin_amdgcn_readfirstlane(blk_raw);
       int64_t row0 = 0;  // cache slot of the tile's first key; block 0 past the end or for an invalid id
@@ -238,7 +242,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
       }
     }
   };
-  auto stage_block = [&](int it) { return tile_block_raw(kParities * it + ld_par); };
+  auto stage_block = [&](int it) { return tile_block_raw(kStageTiles * it + ld_par); };
   auto store_stage = [&](int it, const u32x4 (&r)[kLoadsPerWave]) {
     uint8_t* dst = lds + (it % kStages) * kStageBytes + ld_par * 2 * kTileBytes + (ld_v ? kTileBytes : 0) +
                    ld_slot0 * 1024 + lane * 16;
@@ -346,15 +350,18 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
 
   // ---- pipeline: stage it in LDS, it+1 and it+2 in registers (ra / rb alternate) ----
   auto step = [&](int it) {
-    const int t = kParities * it + par;
-    bool ok = true;
-    if (kPaged && any_bad && t < ntiles) {
-      const int blk = __builtin_amdgcn_readfirstlane(blk_ids[tile_index(t)]);
-      ok = blk >= 0 && blk < p.num_blocks;
-    }
-    if (wave_active && t < ntiles && ok && t * kTile < lim_hi) {
-      const uint8_t* kt = lds + (it % kStages) * kStageBytes + par * 2 * kTileBytes;
-      compute(kt, kt + kTileBytes, t, t * kTile + kTile > lim_lo);
+#pragma unroll
+    for (int sub = 0; sub < kStageTiles; sub += kParities) {
+      const int t = kStageTiles * it + sub + par;
+      bool ok = true;
+      if (kPaged && any_bad && t < ntiles) {
+        const int blk = __builtin_amdgcn_readfirstlane(blk_ids[tile_index(t)]);
+        ok = blk >= 0 && blk < p.num_blocks;
+      }
+      if (wave_active && t < ntiles && ok && t * kTile < lim_hi) {
+        const uint8_t* kt = lds + (it % kStages) * kStageBytes + (sub + par) * 2 * kTileBytes;
+        compute(kt, kt + kTileBytes, t, t * kTile + kTile > lim_lo);
+      }
     }
   };
   u32x4 ra[kLoadsPerWave], rb[kLoadsPerWave];
