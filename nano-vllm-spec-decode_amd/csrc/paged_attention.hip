@@ -32,6 +32,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 
 #include "prefill_attention.h"
@@ -987,15 +988,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // CUs of the current device (the number of 8-wave workgroups it runs at once), queried once per device.
 int wave_slots() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];  // per device; 0 until first queried (threads may race to fill it)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (!cus) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
+    cached[dev].store(cus, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return cus;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
