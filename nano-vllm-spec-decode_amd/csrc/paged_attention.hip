@@ -451,6 +451,7 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
     }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
+      if (rt * 16 + r16 >= rows) continue;  // padding rows are never read (LDS stores are the merge's cost)
       float* orow = ob + (wave * kMergeRows + rt * 16 + r16) * kObRow + 4 * grp;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) *(f32x4*)(orow + 16 * dt) = o[dt][rt];
