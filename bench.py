@@ -9,7 +9,7 @@ launch that rocprofv3's FETCH_SIZE + WRITE_SIZE counters measured for this launc
 profiles/), null if that summary is absent.
 
 Also reported (same JSON line):
-* the verify attention with context lengths uniform in [1024, 8192], and at B in {1, 16} x k in {1, 4, 8};
+* the verify attention with context lengths uniform in [1024, 8192], and at B in {1, 16, 64} x k in {1, 4, 8};
 * the KV-cache scatter (2048 rows, 10% padding slots);
 * the fused q/k RMSNorm + RoPE + KV store over 2048 tokens, next to the reference's eager operations;
 * one draft step's inputs for 64 sequences, next to the reference's tensor operations;
@@ -145,7 +145,7 @@ def bench_verify_uniform(dev, B=64, k=4, lo=1024, hi=8192, W=33):
 
 
 def bench_verify_sweep(dev, ctx_len=4096, W=33):
-    """The other batch / guess-count points of the verify workload at ctx 4096: B in {1, 16}, k in {1, 4, 8},
+    """The batch / guess-count points of the verify workload at ctx 4096: B in {1, 16, 64}, k in {1, 4, 8},
     through Attention.forward's path (planned order), graph-timed over calls that each read the next of
     enough cache copies to exceed the 256 MB last-level cache."""
     import types
@@ -153,7 +153,7 @@ def bench_verify_sweep(dev, ctx_len=4096, W=33):
     from attn_cases import paged_cache, queries
     from nanovllm_amd.layers.attention import paged_decode_attention
     res = {}
-    for B in (1, 16):
+    for B in (1, 16, 64):
         ctx = [ctx_len] * B
         kc, vc, tables = paged_cache(dev, ctx, HKV, D, W=W, seed=0)
         copies = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(max(1, 300 // (17 * B)))]
