@@ -108,9 +108,12 @@ int sd_paged_decode(const void* q, int64_t q_token_stride, const void* k_cache, 
  * sd_paged_decode takes the sequences in index order. sd_paged_decode_plan writes into `workspace` (sized by
  * sd_paged_decode_workspace_size) the sequences sorted by context length, longest first (up to 1024
  * sequences; index order beyond), and sd_paged_decode_planned (same arguments as sd_paged_decode) launches
- * the workgroups in that order, so that long sequences do not end the call alone. The order only decides
- * which workgroup computes which sequence: results are bitwise those of sd_paged_decode even when the
- * plan was made for other context lengths, as long as it was made for the same num_seqs. No counterpart
+ * the workgroups in that order, so that long sequences do not end the call alone. The plan also picks the
+ * K / V load policy of the planned calls: non-temporal when the contexts are balanced (longest at most twice
+ * the mean), the default policy otherwise; sd_paged_decode always loads non-temporal. Order and policy only
+ * decide which workgroup computes which sequence and how it loads: results are bitwise those of
+ * sd_paged_decode even when the plan was made for other context lengths, as long as it was made for the
+ * same num_seqs. No counterpart
  * in the reference; it serves the per-layer loop of a decode step (nanovllm/engine/model_runner.py:476-485).
  */
 int sd_paged_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_query_tokens, int32_t num_heads,

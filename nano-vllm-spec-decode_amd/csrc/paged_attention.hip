@@ -76,6 +76,7 @@ struct Params {
   int64_t num_blocks;
   const int32_t* context_lens;  // decode
   const int32_t* seq_order;     // decode: item i's sequence is seq_order[i / groups_per_seq] (null: i / groups)
+  const int32_t* stream_flag;   // decode: nonzero -> non-temporal K / V loads (null: non-temporal)
   const int32_t* cu_q;          // varlen
   const int32_t* cu_k;          // varlen
   const int32_t* work;          // varlen: (sequence, group) pairs
@@ -157,10 +158,10 @@ __device__ __forceinline__ float quad_sum(float x) {
   return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
 
-// A K / V load of the residue kernel. kStream (decode / verify calls, which read every key once): the
-// non-temporal cache policy; B=64, k=4, ctx 4096 went from 185 to 177 us with it. Varlen calls keep the
-// default policy: their residue items run beside prefill q-blocks that re-read K / V tiles through L2, and
-// the config-5 mixed layer went from 45 to 49 us with non-temporal loads there.
+// A K / V load of the residue kernel. kStream: the non-temporal cache policy, for decode / verify calls
+// whose contexts are balanced (B=64, k=4, ctx 4096: 185 -> 177 us). It costs where a launch ends in a
+// latency-bound tail: decode over unbalanced contexts (lognormal, median 600: 59 -> 63 us) and the varlen /
+// mixed launch (config-5 layer 45 -> 49 us), which therefore keep the default policy (see decode_plan).
 template <bool kStream, class T>
 __device__ __forceinline__ T kv_load(const uint8_t* ptr) {
   if constexpr (kStream)
@@ -179,7 +180,7 @@ __device__ __forceinline__ float merge_scale(float m_r, float M) {
 // One (item, KV head h) with the workgroup's kWaves waves, owning residues bx*kWaves .. +kWaves-1; `lds`
 // holds lds_bytes(kWaves). (kCaller only separates the instantiations made from different kernels: the
 // host compilation pass rejects one instantiation reached from two kernels.)
-template <int RT, bool kVarlen, bool kPaged, int kWaves, int kCaller = 0>
+template <int RT, bool kVarlen, bool kPaged, int kWaves, int kCaller = 0, bool kNT = false>
 __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int item, int h, int bx) {
   constexpr bool kMergeHere = kWaves == kResidues;
   constexpr int kStageBytes = stage_bytes(kWaves);
@@ -308,8 +309,8 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
     const uint32_t off1 = 16 + r16 < ts.nvalid ? k_off1 : 16 * grp;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      kr[0][ks] = kv_load<!kVarlen, bf16x8>(ts.kb + off0 + 64 * ks);
-      kr[1][ks] = kv_load<!kVarlen, bf16x8>(ts.kb + off1 + 64 * ks);
+      kr[0][ks] = kv_load<kNT, bf16x8>(ts.kb + off0 + 64 * ks);
+      kr[1][ks] = kv_load<kNT, bf16x8>(ts.kb + off1 + 64 * ks);
     }
   };
   // V of a tile: 16-byte register loads (lane loads key t = 4*qd + lane/16, chunk (lane%16) ^ 2*(t%8),
@@ -324,7 +325,7 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
     for (int qd = 0; qd < 8; ++qd) {
       const bool valid = 4 * qd + vf_key < ts.nvalid;
       const uint32_t off = (qd % 2) ? (valid ? v_off1 : v_c1) : (valid ? v_off0 : v_c0);
-      vs[qd] = kv_load<!kVarlen, u32x4>(ts.vb + (valid ? (int64_t)(4 * qd) * vsb : 0) + off);
+      vs[qd] = kv_load<kNT, u32x4>(ts.vb + (valid ? (int64_t)(4 * qd) * vsb : 0) + off);
     }
   };
   auto store_v = [&](const u32x4 (&vs)[8], bool ok) {
@@ -515,7 +516,16 @@ __device__ __forceinline__ int rotated_head(const Params& p, int y, int z) {
 template <int RT, bool kVarlen, bool kPaged, int kWaves>
 __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes(kWaves)];
-  attn_body<RT, kVarlen, kPaged, kWaves>(p, lds, blockIdx.z, rotated_head(p, blockIdx.y, blockIdx.z), blockIdx.x);
+  const int h = rotated_head(p, blockIdx.y, blockIdx.z);
+  if constexpr (kVarlen) {
+    attn_body<RT, kVarlen, kPaged, kWaves>(p, lds, blockIdx.z, h, blockIdx.x);
+  } else {
+    // one uniform branch per workgroup between two copies of the body (load policy only)
+    if (p.stream_flag == nullptr || *p.stream_flag != 0)
+      attn_body<RT, kVarlen, kPaged, kWaves, 0, true>(p, lds, blockIdx.z, h, blockIdx.x);
+    else
+      attn_body<RT, kVarlen, kPaged, kWaves, 0, false>(p, lds, blockIdx.z, h, blockIdx.x);
+  }
 }
 
 // Few (item, KV head) pairs (one-residue workgroups): the residue body with one wave keeps one 16 KB tile in
@@ -977,24 +987,50 @@ __global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __res
 // longest (sequence, KV head) workgroups are dispatched first and short ones fill the tail; up to
 // kPlanThreads sequences (more: index order). Any permutation gives the same results: only which workgroup
 // computes an item changes.
+// Also writes order[num_seqs], the load-policy flag of the attention calls that use the plan: 1
+// (non-temporal K / V loads) when the contexts are balanced, longest at most twice the mean, so that the call
+// stays bandwidth-bound to its end; 0 when a few long contexts would leave a latency-bound tail.
 __global__ __launch_bounds__(kPlanThreads) void decode_plan(const int32_t* __restrict__ context_lens, int32_t num_seqs,
                                                             int32_t* __restrict__ order) {
   __shared__ uint32_t keys[kPlanThreads];
+  __shared__ int64_t wsum[kPlanThreads / kWave];
+  __shared__ int32_t wmax[kPlanThreads / kWave];
   const int tid = threadIdx.x;
   if (num_seqs > kPlanThreads) {
     for (int i = tid; i < num_seqs; i += kPlanThreads) order[i] = i;
+    if (tid == 0) order[num_seqs] = 1;
     return;
   }
   uint32_t key = 0xFFFFFFFFu;
+  int L = 0;
   if (tid < num_seqs) {
-    const int L = max(context_lens[tid], 0);
+    L = max(context_lens[tid], 0);
     const uint32_t tiles = min((uint32_t)(L + kTile - 1) / kTile, (1u << 20) - 1);
     key = (((1u << 20) - 1 - tiles) << 10) | (uint32_t)tid;
   }
   keys[tid] = key;
+  int64_t sum = L;
+  int mx = L;
+  for (int off = 32; off >= 1; off >>= 1) {
+    sum += __shfl_xor(sum, off);
+    mx = max(mx, __shfl_xor(mx, off));
+  }
+  if (tid % kWave == 0) {
+    wsum[tid / kWave] = sum;
+    wmax[tid / kWave] = mx;
+  }
   __syncthreads();
   bitonic_sort(keys, sort_width(num_seqs));
   if (tid < num_seqs) order[tid] = (int32_t)(keys[tid] & 1023u);
+  if (tid == 0) {
+    int64_t total = 0;
+    int longest = 0;
+    for (int w = 0; w < kPlanThreads / kWave; ++w) {
+      total += wsum[w];
+      longest = max(longest, wmax[w]);
+    }
+    order[num_seqs] = (int64_t)longest * num_seqs <= 2 * total ? 1 : 0;
+  }
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -1031,7 +1067,7 @@ Layout workspace_layout(int64_t items, int Hkv, int rows_alloc, bool partials, b
   L.work_pre = align256(L.count + (varlen ? sizeof(int32_t) : 0));
   L.count_pre = align256(L.work_pre + (varlen ? (size_t)pre_items * 2 * sizeof(int32_t) : 0));
   L.order = align256(L.count_pre + (varlen ? sizeof(int32_t) : 0));
-  L.total = align256(L.order + (size_t)order_len * sizeof(int32_t));
+  L.total = align256(L.order + (size_t)(order_len ? order_len + 1 : 0) * sizeof(int32_t));  // + load-policy flag
   return L;
 }
 
@@ -1187,6 +1223,7 @@ int decode_run(const char* who, bool planned, const void* q, int64_t q_token_str
   p.part_o = partials ? (float*)((uint8_t*)workspace + lay.part_o) : nullptr;
   p.part_ml = partials ? (float*)((uint8_t*)workspace + lay.part_ml) : nullptr;
   p.seq_order = planned ? (const int32_t*)((uint8_t*)workspace + lay.order) : nullptr;
+  p.stream_flag = planned ? p.seq_order + num_seqs : nullptr;
 
   hipStream_t s = (hipStream_t)stream;
   launch_fwd<false, true>(RT, waves, dim3(1, num_kv_heads, (unsigned)items), s, p);
