@@ -40,8 +40,10 @@ def test_abi_version(lib):
 
 def test_workspace_sizes(lib):
     # 64 sequences x 8 kv heads = 512 (item, head) pairs fill the GPU with 8-wave workgroups that merge
-    # their residues in LDS: no partials, only the planned call's sequence order (64 int32, 256-B aligned).
-    assert lib.sd_paged_decode_workspace_size(64, 5, 32, 8, 128, 256, 33) == 256
+    # their residues in LDS: no partials, only the planned call's sequence order (64 int32) and its load-policy
+    # flag (one int32), 256-B aligned.
+    assert lib.sd_paged_decode_workspace_size(64, 5, 32, 8, 128, 256, 33) == 512
+    assert lib.sd_paged_decode_workspace_size(63, 5, 32, 8, 128, 256, 33) == 256
     # 16 sequences: residue partials [16 items][8 heads][8 residues][32 rows] x (128 + 2) fp32
     assert lib.sd_paged_decode_workspace_size(16, 5, 32, 8, 128, 256, 33) >= 16 * 8 * 8 * 32 * 130 * 4
     # 9 queries x 4 heads = 36 rows -> 3 row tiles, which never merge in LDS
