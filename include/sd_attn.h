@@ -174,10 +174,13 @@ int sd_varlen_attention_planned(const void* q, int64_t q_token_stride, const voi
  * temperatures, draft_logits), nanovllm/layers/sampler.py:28-103, with the reference's internal
  * torch.rand(S, K) and exponential_(1) [S, V] passed in as `uniforms` and `exp_noise`.
  * logits: [S*(K+1), vocab] rows (row stride in elements), dtype SD_DTYPE_BF16 or SD_DTYPE_F32.
- * draft_token_ids int64 [S, K]; num_drafts int64 [S]; temperatures fp32 [S] (0 = greedy).
+ * draft_token_ids int64 [S, K]; num_drafts int64 [S]; temperatures fp32 [S] (0 = greedy), or NULL when
+ * every row is greedy: then only the argmax pass and the decision run (two launches instead of four).
  * draft_logits: [S*K, vocab] rows or NULL (n-gram: q is one-hot on the guess).
  * uniforms fp32 [S, K] and exp_noise fp32 [S, vocab] are read only for rows with temperature != 0
- * (may be NULL when every temperature is 0).
+ * (may be NULL when every temperature is 0; a NULL one reads as u = 1 / E = 1).
+ * Logsumexp and softmax statistics follow torch.logsumexp's rule (shift by the row maximum, 0 when that is
+ * infinite); every exponential is computed to about 1.5 ulp.
  * Outputs num_accepted int64 [S] and next_token int64 [S].
  */
 size_t sd_verify_workspace_size(int32_t num_seqs, int32_t num_draft_slots, int32_t vocab,
@@ -210,6 +213,7 @@ int sd_draft_step_inputs(const int32_t* real_lens, const int64_t* last_positions
  * Token sampler. Replaces Sampler.forward(logits, temperatures), nanovllm/layers/sampler.py:5-16, with
  * the internal exponential_(1) noise passed in as exp_noise fp32 [S, vocab] (NULL if all greedy).
  * Greedy rows (temperature 0) take the first argmax; the others argmax(softmax(l/T) / max(E, 1e-10)).
+ * temperatures may be NULL when every row is greedy (argmax pass only).
  */
 int sd_sample(const void* logits, int32_t logits_dtype, int64_t logits_row_stride, const float* temperatures,
               const float* exp_noise, int32_t num_seqs, int32_t vocab, int64_t* next_token, void* workspace,

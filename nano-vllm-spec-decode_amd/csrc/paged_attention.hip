@@ -1319,7 +1319,8 @@ VarlenShape varlen_shape(int32_t num_seqs, int32_t total_q, int32_t max_seqlen_q
   v.items = varlen_items(num_seqs, total_q, v.P);
   v.pre_items = prefill_items(num_seqs, total_q, max_seqlen_q, prefill_positions(v.g));
   v.waves = residue_waves(v.items, Hkv, kVarlenRT);
-  v.partials = v.waves < kResidues;
+  // With prefill items the call is one mixed_fwd launch, whose residue items always merge in LDS: no partials.
+  v.partials = v.waves < kResidues && v.pre_items == 0;
   v.lay = workspace_layout(v.items, Hkv, 16 * kVarlenRT, v.partials, true, v.pre_items);
   return v;
 }
@@ -1342,9 +1343,12 @@ extern "C" size_t sd_varlen_workspace_size(int32_t num_seqs, int32_t total_q, in
   const int g = num_heads / num_kv_heads;
   const int P = varlen_positions(g);
   const int64_t items = varlen_items(num_seqs, total_q, P);
+  // The larger of the two launch forms: residue items alone (partials when they are few), or with the most
+  // prefill items any max_seqlen_q allows (no partials).
   const int64_t pre_items = g <= 16 * kVarlenRT ? prefill_items(num_seqs, total_q, INT_MAX, prefill_positions(g)) : 0;
   const bool partials = residue_waves(items, num_kv_heads, kVarlenRT) < kResidues;
-  return workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true, pre_items).total;
+  return std::max(workspace_layout(items, num_kv_heads, 16 * kVarlenRT, partials, true, 0).total,
+                  workspace_layout(items, num_kv_heads, 16 * kVarlenRT, false, true, pre_items).total);
 }
 
 namespace {

@@ -32,8 +32,8 @@ constexpr int kSpans = 8;         // most spans per row (workgroups per row)
 constexpr int kThreads = 256;
 
 struct RowStat {                  // per (row, chunk)
-  float max_x;                    // max of l / T over the chunk (random rows)
-  float sum;                      // sum of exp(l / T - max_x) (random rows)
+  float max_x;                    // max of l / T over the chunk (random rows; -inf for an all -inf chunk)
+  float sum;                      // sum of exp(l / T - lse_shift(max_x)) (random rows)
   float best;                     // raw logit at the chunk's first argmax (target rows)
   int32_t best_idx;
 };
@@ -44,8 +44,8 @@ struct SeqInfo {
   int32_t resid_mode;             // 0: sample from p; 1: n-gram (zero the guess if rejected); 2: draft residual
   int32_t rejected;               // a < num_drafts
   int32_t guess;                  // guess token of the rejected slot (n-gram), or -1
-  float Ma, Sa;                   // softmax stats of target row a
-  float Md, Sd;                   // softmax stats of the draft row of the rejected slot
+  float Ma, Sa;                   // softmax of target row a: shift lse_shift(max) and sum of exp(x - shift)
+  float Md, Sd;                   // the same for the draft row of the rejected slot
   float pad[3];
 };
 
@@ -80,26 +80,48 @@ __device__ __forceinline__ float4 load_logit4(const void* base, int64_t idx) {
                      __builtin_bit_cast(float, w.y << 16), __builtin_bit_cast(float, w.y & 0xffff0000u));
 }
 
-// exp(x) as one v_exp_f32 of x * log2(e): for the per-entry exponentials of the streaming kernels. Its
-// relative error (the rounding of the product, about |x| * 2^-24) stays near 1e-6 over the range softmax
-// sees; the few exponentials of the merges keep expf.
-__device__ __forceinline__ float exp_entry(float x) { return exp2_fast(x * 1.4426950408889634f); }
+// exp(x) to about 1.5 ulp, for every exponential of the sampler: x*log2(e) is split into an integer n and a
+// fraction f, the product's rounding error carried into f by two fma (log2(e) as a pair of floats), then
+// 2^f from v_exp_f32 (1 ulp on [-0.5, 0.5]) scaled by 2^n. Inputs are clamped to [-110, 100], where exp
+// already rounds to 0 or overflows to inf (NaN stays NaN).
+// Contraction is off here: fusing the product t into (t - n) would count its rounding error twice.
+__device__ __forceinline__ float exp_acc(float x) {
+#pragma clang fp contract(off)
+  x = x < -110.f ? -110.f : (x > 100.f ? 100.f : x);
+  const float kHi = 1.44269502162933349609375f;   // log2(e) rounded to fp32
+  const float kLo = 1.925963033500011e-08f;       // log2(e) - kHi
+  const float t = x * kHi;
+  const float n = __builtin_rintf(t);
+  const float f = (t - n) + fmaf(x, kLo, fmaf(x, kHi, -t));
+  return ldexpf(__builtin_amdgcn_exp2f(f), (int)n);
+}
 
-// Online (max, sum of exp(x - max)) of one thread's entries; an infinite or empty max uses 0 as the shift.
+// The shift of a logsumexp: the maximum, or 0 when it is infinite (torch.logsumexp's rule), so that
+// an all -inf set sums to 0 (lse -inf) and a +inf entry gives +inf.
+__device__ __forceinline__ float lse_shift(float m) { return fabsf(m) == INFINITY ? 0.f : m; }
+
+// Online (max m, sum s of exp(x - lse_shift(m))) of one thread's entries. s == 0 exactly while every entry
+// seen is -inf; a rescale is skipped then (it would multiply 0 by an overflowing factor).
 struct OnlineSum {
   float m = -INFINITY, s = 0.f;
-  __device__ __forceinline__ float shift() const { return fabsf(m) == INFINITY ? 0.f : m; }
   __device__ __forceinline__ void add4(float x0, float x1, float x2, float x3) {
     const float ml = fmaxf(fmaxf(x0, x1), fmaxf(x2, x3));
     if (ml > m) {
-      const float old = shift();
+      if (s != 0.f) s *= exp_acc(lse_shift(m) - lse_shift(ml));
       m = ml;
-      s *= exp_entry(old - shift());
     }
-    const float sh = shift();
-    s += exp_entry(x0 - sh) + exp_entry(x1 - sh) + exp_entry(x2 - sh) + exp_entry(x3 - sh);
+    const float sh = lse_shift(m);
+    s += exp_acc(x0 - sh) + exp_acc(x1 - sh) + exp_acc(x2 - sh) + exp_acc(x3 - sh);
   }
 };
+
+// (m, s) of two disjoint sets merged: the sum rescaled to the larger max; an empty side (s == 0) adds 0.
+__device__ __forceinline__ void merge_pair(float& m, float& s, float om, float os) {
+  const float M = fmaxf(m, om);
+  const float shM = lse_shift(M);
+  s = (s != 0.f ? s * exp_acc(lse_shift(m) - shM) : 0.f) + (os != 0.f ? os * exp_acc(lse_shift(om) - shM) : 0.f);
+  m = M;
+}
 
 // Block-wide reductions over 256 threads (4 waves) in a fixed order.
 __device__ __forceinline__ float block_max(float v, float* sh) {
@@ -124,11 +146,7 @@ __device__ __forceinline__ float block_sum(float v, float* sh) {
 __device__ __forceinline__ void combine_online(OnlineSum& o, float* sh) {
   for (int off = 32; off >= 1; off >>= 1) {
     const float om = __shfl_xor(o.m, off), os = __shfl_xor(o.s, off);
-    const float M = fmaxf(o.m, om);
-    const float sh_ = fabsf(M) == INFINITY ? 0.f : M;
-    const float a = fabsf(o.m) == INFINITY ? 0.f : o.m, b = fabsf(om) == INFINITY ? 0.f : om;
-    o.s = o.s * expf(a - sh_) + os * expf(b - sh_);
-    o.m = M;
+    merge_pair(o.m, o.s, om, os);
   }
   const int w = threadIdx.x / kWave;
   __syncthreads();
@@ -137,14 +155,8 @@ __device__ __forceinline__ void combine_online(OnlineSum& o, float* sh) {
     sh[2 * w + 1] = o.s;
   }
   __syncthreads();
-  float M = -INFINITY;
-  for (int k = 0; k < 4; ++k) M = fmaxf(M, sh[2 * k]);
-  const float shM = fabsf(M) == INFINITY ? 0.f : M;
-  float S = 0.f;
-  for (int k = 0; k < 4; ++k) {
-    const float mk = sh[2 * k];
-    S += sh[2 * k + 1] * expf((fabsf(mk) == INFINITY ? 0.f : mk) - shM);
-  }
+  float M = sh[0], S = sh[1];
+  for (int k = 1; k < 4; ++k) merge_pair(M, S, sh[2 * k], sh[2 * k + 1]);
   o.m = M;
   o.s = S;
 }
@@ -179,7 +191,7 @@ struct VParams {
   int64_t logits_stride;
   const int64_t* drafts;          // [S, K]
   const int64_t* num_drafts;      // [S]
-  const float* temps;             // [S]
+  const float* temps;             // [S], or null: every row greedy
   const void* draft_logits;       // [S*K] rows or null
   int64_t draft_stride;
   const float* uniforms;          // [S, K]
@@ -193,7 +205,7 @@ struct VParams {
   Cand* cand;                     // [S][rchunk]
 };
 
-template <int DT, int DDT, bool kVec>
+template <int DT, int DDT, bool kVec, bool kRand>
 __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
   __shared__ float shf[8];
   __shared__ int shi[4];
@@ -202,8 +214,8 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
   const int target_rows = p.S * (p.K + 1);
   const bool is_target = row < target_rows;
   const int seq = is_target ? row / (p.K + 1) : (row - target_rows) / p.K;
-  const float T = p.temps[seq];
-  const bool random = T != 0.f;
+  const float T = kRand ? p.temps[seq] : 0.f;
+  const bool random = kRand && T != 0.f;
   if (!is_target && !random) return;  // draft rows only matter for sampled rows
   const void* base;
   if (is_target) {
@@ -271,30 +283,34 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
     body(v, r);
   }
   RowStat st;
-  st.max_x = 0.f;
+  st.max_x = -INFINITY;
   st.sum = 0.f;
   if (is_target) block_argmax(bv, bi, shf, shi);
   st.best = bv;
   st.best_idx = bi;
   if (random) {
     combine_online(os, shf);
-    st.max_x = fabsf(os.m) == INFINITY ? 0.f : os.m;
+    st.max_x = os.m;
     st.sum = os.s;
   }
   if (threadIdx.x == 0) p.stats[(int64_t)row * p.nchunk + chunk] = st;
 }
 
-// Merged (max, sum) of a row's chunks, in chunk order: sum = sum_c sum_c * exp(max_c - M).
-__device__ void merge_softmax(const RowStat* st, int nchunk, float* M_out, float* S_out) {
+// A row's softmax statistics from its chunks, in chunk order: the shift lse_shift(max over chunks) and
+// sum = sum_c sum_c * exp(lse_shift(max_c) - shift); chunks whose entries are all -inf (sum 0) add nothing.
+// logsumexp = log(sum) + shift (-inf for an all -inf row).
+__device__ void merge_softmax(const RowStat* st, int nchunk, float* shift_out, float* S_out) {
   float M = -INFINITY;
   for (int c = 0; c < nchunk; ++c) M = fmaxf(M, st[c].max_x);
+  const float shM = lse_shift(M);
   float s = 0.f;
-  for (int c = 0; c < nchunk; ++c) s += st[c].sum * expf(st[c].max_x - M);
-  *M_out = M;
+  for (int c = 0; c < nchunk; ++c)
+    if (st[c].sum != 0.f) s += st[c].sum * exp_acc(lse_shift(st[c].max_x) - shM);
+  *shift_out = shM;
   *S_out = s;
 }
 
-template <int DT, int DDT>
+template <int DT, int DDT, bool kRand>
 __global__ __launch_bounds__(64) void verify_decide(VParams p) {
   __shared__ int32_t top1[65];
   __shared__ float lse[65];
@@ -302,8 +318,8 @@ __global__ __launch_bounds__(64) void verify_decide(VParams p) {
   const int seq = blockIdx.x;
   const int lane = threadIdx.x;
   const int K = p.K;
-  const float T = p.temps[seq];
-  const bool random = T != 0.f;
+  const float T = kRand ? p.temps[seq] : 0.f;
+  const bool random = kRand && T != 0.f;
   const int target_rows = p.S * (K + 1);
   for (int j = lane; j <= K; j += 64) {
     const RowStat* st = p.stats + (int64_t)(seq * (K + 1) + j) * p.nchunk;
@@ -343,14 +359,14 @@ __global__ __launch_bounds__(64) void verify_decide(VParams p) {
         const float xl = (DT == SD_DTYPE_F32)
                              ? ((const float*)p.logits)[(int64_t)(seq * (K + 1) + j) * p.logits_stride + d]
                              : bf16_bits_to_f32(((const uint16_t*)p.logits)[(int64_t)(seq * (K + 1) + j) * p.logits_stride + d]);
-        const float pd = expf(xl / T - lse[j]);
+        const float pd = exp_acc(xl / T - lse[j]);
         float qd = 1.f;
         if (p.draft_logits) {
           const int64_t dr = (int64_t)seq * K + j;
           const float xd = (DDT == SD_DTYPE_F32)
                                ? ((const float*)p.draft_logits)[dr * p.draft_stride + d]
                                : bf16_bits_to_f32(((const uint16_t*)p.draft_logits)[dr * p.draft_stride + d]);
-          qd = expf(xd / T - dlse[j]);
+          qd = exp_acc(xd / T - dlse[j]);
         }
         const float u = p.uniforms ? p.uniforms[(int64_t)seq * K + j] : 1.f;  // missing uniforms: u = 1
         acc = u * qd < pd;
@@ -449,7 +465,7 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
     for (int e = 0; e < 4; ++e) {
       const int idx = v + e;
       if (idx >= v1) continue;
-      float prob = exp_entry((T == 1.f ? l[e] : l[e] / T) - info.Ma) / info.Sa;  // divided, as softmax does
+      float prob = exp_acc((T == 1.f ? l[e] : l[e] / T) - info.Ma) / info.Sa;
       const float Ee = noise ? fmaxf(E[e], 1e-10f) : 1.f;
       if (info.resid_mode == 1 && info.rejected && idx == info.guess) prob = 0.f;
       const float sp = prob / Ee;
@@ -458,7 +474,7 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
         pi = idx;
       }
       if (dbase) {
-        const float q = exp_entry((T == 1.f ? ld[e] : ld[e] / T) - info.Md) / info.Sd;
+        const float q = exp_acc((T == 1.f ? ld[e] : ld[e] / T) - info.Md) / info.Sd;
         const float res = fmaxf(prob - q, 0.f);
         any_res |= res > 0.f;
         const float sr = res / Ee;
@@ -562,13 +578,20 @@ VLayout verify_layout(int S, int K, int V, bool draft) {
   return L;
 }
 
+// Greedy-only calls (no temperatures) run the argmax pass and the decision alone.
 template <int DT, int DDT, bool kVec>
 int launch_all(const VParams& p, hipStream_t s, bool draft) {
   int rc;
+  if (!p.temps) {
+    hipLaunchKernelGGL((row_stats<DT, DDT, kVec, false>), dim3(p.S * (p.K + 1), p.nchunk), dim3(kThreads), 0, s, p);
+    if ((rc = check_launch("row_stats"))) return rc;
+    hipLaunchKernelGGL((verify_decide<DT, DDT, false>), dim3(p.S), dim3(64), 0, s, p);
+    return check_launch("verify_decide");
+  }
   const int rows = p.S * (p.K + 1) + (draft ? p.S * p.K : 0);
-  hipLaunchKernelGGL((row_stats<DT, DDT, kVec>), dim3(rows, p.nchunk), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL((row_stats<DT, DDT, kVec, true>), dim3(rows, p.nchunk), dim3(kThreads), 0, s, p);
   if ((rc = check_launch("row_stats"))) return rc;
-  hipLaunchKernelGGL((verify_decide<DT, DDT>), dim3(p.S), dim3(64), 0, s, p);
+  hipLaunchKernelGGL((verify_decide<DT, DDT, true>), dim3(p.S), dim3(64), 0, s, p);
   if ((rc = check_launch("verify_decide"))) return rc;
   hipLaunchKernelGGL((verify_resample<DT, DDT, kVec>), dim3(p.S, p.rchunk), dim3(kThreads), 0, s, p);
   if ((rc = check_launch("verify_resample"))) return rc;
@@ -584,7 +607,7 @@ int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_
   if (S < 0 || K < 0 || K > 63 || V <= 0)
     return fail(kBadArgument, "%s: bad sizes (seqs %d, draft slots %d (max 63), vocab %d)", who, S, K, V);
   if (S == 0) return kOk;
-  if (!logits || !temps || !out_next || (K > 0 && (!drafts || !num_drafts)))
+  if (!logits || !out_next || (K > 0 && (!drafts || !num_drafts)))
     return fail(kBadArgument, "%s: null pointer", who);
   if (logits_dtype != SD_DTYPE_BF16 && logits_dtype != SD_DTYPE_F32)
     return fail(kUnsupported, "%s: logits dtype %d not supported", who, logits_dtype);

@@ -128,8 +128,11 @@ class MixedStepRunner:
         self._meta = torch.zeros(meta_len, dtype=torch.int32, device=dev)
         self._staging = torch.zeros(meta_len, dtype=torch.int32, pin_memory=True)
         lib = _lib.load()
-        self._ws_bytes = lib.sd_varlen_workspace_size(Smax, Nmax, table_width * block_size, num_heads,
-                                                      num_kv_heads, head_dim)
+        # The varlen workspace is not monotone in the bucket (few work items need residue partials), so it is
+        # sized for the largest need over every (token, sequence) bucket.
+        self._ws_bytes = max(lib.sd_varlen_workspace_size(S, N, table_width * block_size, num_heads, num_kv_heads,
+                                                          head_dim)
+                             for N in self.token_buckets for S in self.seq_buckets)
         self._ws = torch.empty(max(self._ws_bytes, 256), dtype=torch.uint8, device=dev)
         self._copied = torch.cuda.Event()  # the last staging copy has been read (the buffer is free again)
         self._copied.record(torch.cuda.current_stream(self.device))

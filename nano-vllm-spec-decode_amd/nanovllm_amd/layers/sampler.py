@@ -44,12 +44,15 @@ def verify_drafts(logits: torch.Tensor, draft_token_ids: torch.Tensor, num_draft
     drows = _rows(draft_logits, V) if draft_logits is not None and K > 0 else None
     if drows is not None and drows.size(0) != S * K:
         raise ValueError("verify_drafts: draft_logits must hold S*K rows")
+    all_greedy = False
     if uniforms is None or exp_noise is None:
         if _any_random(temps):
             if uniforms is None and K > 0:
                 uniforms = torch.rand(S, K, device=device, dtype=torch.float32)
             if exp_noise is None:
                 exp_noise = torch.empty(S, V, device=device, dtype=torch.float32).exponential_(1)
+        else:
+            all_greedy = True    # the argmax pass alone decides every row
     if uniforms is not None:
         uniforms = uniforms.float().contiguous()
     if exp_noise is not None:
@@ -62,7 +65,8 @@ def verify_drafts(logits: torch.Tensor, draft_token_ids: torch.Tensor, num_draft
     nbytes = lib.sd_verify_workspace_size(S, K, V, int(drows is not None))
     ws = _lib.workspace(nbytes, device)
     rc = lib.sd_verify_drafts(rows.data_ptr(), _DTYPES[rows.dtype], rows.stride(0), drafts.data_ptr(), nd.data_ptr(),
-                              temps.data_ptr(), _lib.ptr(drows), _DTYPES[drows.dtype] if drows is not None else 0,
+                              None if all_greedy else temps.data_ptr(), _lib.ptr(drows),
+                              _DTYPES[drows.dtype] if drows is not None else 0,
                               drows.stride(0) if drows is not None else 0, _lib.ptr(uniforms), _lib.ptr(exp_noise),
                               S, K, V, num_accepted.data_ptr(), next_token.data_ptr(), ws.data_ptr(), ws.numel(),
                               _lib.stream_of(device))

@@ -12,7 +12,7 @@ import torch
 from nanovllm_amd.engine.mixed_step import MixedStepRunner
 from nanovllm_amd.layers.attention import store_kvcache, varlen_attention
 from attn_cases import BLOCK, paged_cache, queries
-from test_gpu_varlen import mixed_step
+from nanovllm_amd.engine.synthetic import mixed_step_lengths as mixed_step, requests
 
 pytestmark = pytest.mark.gpu
 
@@ -21,20 +21,7 @@ LAYERS = 3
 
 
 def _requests(lq, lk, tables, nd):
-    """Sequence objects (the fields mixed_batch reads) for nd decode requests then prefill chunks."""
-    seqs = []
-    for s, (a, c) in enumerate(zip(lq, lk)):
-        blocks = [int(x) for x in tables[s, :math.ceil(c / BLOCK)].tolist()]
-        if s < nd:   # decode: Lk = num_tokens + k
-            n = c - K
-            seqs.append(SimpleNamespace(token_ids=[7] * n, last_token=7, num_tokens=n, num_cached_tokens=n - 1,
-                                        num_scheduled_tokens=1, is_prefill=False, block_table=blocks,
-                                        draft_token_ids=[3] * K))
-        else:        # prefill chunk: Lk = cached + scheduled
-            seqs.append(SimpleNamespace(token_ids=[5] * (c + 1), last_token=5, num_tokens=c + 1,
-                                        num_cached_tokens=c - a, num_scheduled_tokens=a, is_prefill=True,
-                                        block_table=blocks, draft_token_ids=[]))
-    return seqs
+    return requests(lq, lk, tables, nd, K, BLOCK)
 
 
 def _eager(layout, q, k, v, caches, W):
@@ -159,3 +146,126 @@ def test_mixed_step_with_fused_pre_attention(device):
         for l, ((gk, gv), (ek, ev)) in enumerate(zip(graph_caches, eager_caches)):
             assert torch.equal(gk, ek) and torch.equal(gv, ev), f"step {i} layer {l}: caches differ"
     assert len(runner.graphs) == 1
+
+
+class _RecordingSegment:
+    """Segment i writes seeded q / k / v rows for layer i (per token, no metadata); with `record` set it also
+    keeps copies of what it wrote and of bufs["o"] (layer i-1's attention output) for the oracle."""
+
+    def __init__(self, device, n_layers, seed):
+        self.L, self.record, self.seen = n_layers, False, {}
+        self.qkv = [(queries(device, 2048, HQ, D, seed=seed + 3 * i), queries(device, 2048, HKV, D, seed=seed + 3 * i + 1),
+                     queries(device, 2048, HKV, D, seed=seed + 3 * i + 2)) for i in range(n_layers)]
+
+    def __call__(self, i, n, bufs):
+        if self.record and i > 0:
+            self.seen[("o", i - 1)] = bufs["o"][:n].clone()
+        if i == self.L:
+            return
+        for name, src in zip("qkv", self.qkv[i]):
+            bufs[name][:n].copy_(src[:n])
+            if self.record:
+                self.seen[(name, i)] = src[:n].clone()
+
+
+def _oracle_layers(layout, seg, caches_cpu, W):
+    """Per layer: oracle store of the layer's k / v rows, then oracle varlen attention of its q rows."""
+    from oracle import attention as oatt
+    from oracle import kvcache as okv
+    n, S = layout["n"], layout["S"]
+    Sr = len(layout["cu_seqlens_q"]) - 1
+    cu_q = torch.tensor(layout["cu_seqlens_q"], dtype=torch.int32)
+    cu_k = torch.tensor(layout["cu_seqlens_k"], dtype=torch.int32)
+    slots = torch.tensor(layout["slot_mapping"], dtype=torch.int32)
+    tab = torch.tensor(layout["meta"][2 * (S + 1) + layout["N"]:], dtype=torch.int32).view(S, W)[:Sr]
+    outs = []
+    for i, (kc, vc) in enumerate(caches_cpu):
+        q, k, v = (seg.seen[(x, i)].cpu()[:n] for x in "qkv")
+        okv.store_kvcache(k, v, kc, vc, slots)
+        outs.append(oatt.varlen_attention(q, kc, vc, cu_q, cu_k, D ** -0.5, tab))
+    return outs
+
+
+@pytest.mark.parametrize("case", ["config5", "one_chunk_one_verify", "decode_only_two"])
+def test_mixed_step_runner_vs_oracle(device, case):
+    """MixedStepRunner with a segment callback, eager: every layer's attention output against the oracle's
+    varlen attention (max-abs 2e-2, mean-abs 2e-3) and the KV caches against the oracle's store, bitwise;
+    then the same step replayed from the bucket's graph equals the eager run bitwise. The small cases run in
+    small buckets, whose residue work lists are short."""
+    from attn_cases import error_stats
+    if case == "config5":
+        lq, lk = mixed_step(4)
+        nd = 48
+    elif case == "one_chunk_one_verify":
+        lq, lk, nd = [K + 1, 37], [700, 37 + 300], 1
+    else:
+        lq, lk, nd = [K + 1, K + 1], [1000, 260], 2
+    W = math.ceil(max(lk) / BLOCK)
+    kc, vc, tables = paged_cache(device, lk, HKV, D, W=W, seed=9)
+    caches = [(kc.clone(), vc.clone()) for _ in range(LAYERS)]
+    caches_cpu = [(kc.cpu(), vc.cpu()) for _ in range(LAYERS)]
+    layers = [SimpleNamespace(k_cache=a, v_cache=b) for a, b in caches]
+    seg = _RecordingSegment(device, LAYERS, seed=60)
+    runner = MixedStepRunner(layers, HQ, HKV, D, D ** -0.5, block_size=BLOCK, max_num_batched_tokens=2048,
+                             max_num_seqs=64, table_width=W, segment=seg)
+    layout = runner.prepare(_requests(lq, lk, tables.cpu(), nd), K)
+    n, N = layout["n"], layout["N"]
+    print(f"{case}: {n} tokens, {len(lq)} sequences in bucket ({N}, {layout['S']})", flush=True)
+    seg.record = True
+    eager = runner.run(layout, use_graph=False).clone()
+    seg.record = False
+    torch.cuda.synchronize()
+    refs = _oracle_layers(layout, seg, caches_cpu, W)
+    for i, ref in enumerate(refs):
+        got = seg.seen[("o", i)][:n]
+        mx, mean = error_stats(got, ref)
+        print(f"  layer {i}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
+        assert mx <= 2e-2 and mean <= 2e-3, (case, i, mx, mean)
+    assert torch.equal(eager, seg.seen[("o", LAYERS - 1)][:n])
+    for i, ((gk, gv), (ok, ov)) in enumerate(zip(caches, caches_cpu)):
+        assert torch.equal(gk.cpu(), ok) and torch.equal(gv.cpu(), ov), f"layer {i}: caches differ from the oracle"
+    first = runner.run(layout).clone()     # records the graph (its warm-up runs the step again: same stores)
+    replay = runner.run(layout).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(first, eager) and torch.equal(replay, eager)
+    for i, ((gk, gv), (ok, ov)) in enumerate(zip(caches, caches_cpu)):
+        assert torch.equal(gk.cpu(), ok) and torch.equal(gv.cpu(), ov), f"layer {i}: caches changed on replay"
+
+
+def test_mixed_step_qwen3_segments_graph_equals_eager(device):
+    """The piecewise step with model segments: a random-init Qwen3-8B-shaped stack (3 layers) recorded into
+    the step's graph with the fused pre-attention kernel. The graph replay equals the same body run eagerly,
+    bitwise, in the hidden states and in every layer's KV cache; a second step with other token ids in the
+    same bucket replays the graph and again equals its eager run."""
+    from nanovllm_amd.engine.qwen3_segments import Qwen3Segments
+    lq, lk = mixed_step(5)
+    nd = 48
+    W = math.ceil(max(lk) / BLOCK)
+    kc, vc, tables = paged_cache(device, lk, HKV, D, W=W, seed=11)
+    graph_caches = [(kc.clone(), vc.clone()) for _ in range(LAYERS)]
+    eager_caches = [(kc.clone(), vc.clone()) for _ in range(LAYERS)]
+    del kc, vc
+    seg = Qwen3Segments(num_layers=LAYERS, device=device, seed=3)
+    mk = lambda caches: MixedStepRunner([SimpleNamespace(k_cache=a, v_cache=b) for a, b in caches], HQ, HKV, D,
+                                        D ** -0.5, block_size=BLOCK, max_num_seqs=64, table_width=W, segment=seg,
+                                        pre_attn=seg.pre_attn())
+    graph_runner, eager_runner = mk(graph_caches), mk(eager_caches)
+    layout = graph_runner.prepare(_requests(lq, lk, tables.cpu(), nd), K)
+    n, N = layout["n"], layout["N"]
+    g = torch.Generator(device=device).manual_seed(12)
+    for step in range(2):
+        ids = torch.randint(0, 151936, (N,), device=device, generator=g)
+        ids[n:] = 0
+        seg.input_ids[:N] = ids
+        graph_runner.run(layout)
+        hg = seg.hidden_out[:n].clone()
+        seg.input_ids[:N] = ids
+        eager_runner.run(layout, use_graph=False)
+        he = seg.hidden_out[:n].clone()
+        torch.cuda.synchronize()
+        print(f"step {step}: {n} tokens, hidden |mean| {he.float().abs().mean().item():.3f}", flush=True)
+        assert torch.isfinite(he.float()).all()
+        assert torch.equal(hg, he), f"step {step}: graph hidden states differ from the eager body"
+        for i, ((a, b), (c, d)) in enumerate(zip(graph_caches, eager_caches)):
+            assert torch.equal(a, c) and torch.equal(b, d), f"step {step} layer {i}: caches differ"
+    assert len(graph_runner.graphs) == 1

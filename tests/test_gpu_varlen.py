@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+from nanovllm_amd.engine.synthetic import mixed_step_lengths as mixed_step
 from nanovllm_amd.layers.attention import paged_decode_attention, varlen_attention
 from oracle import attention as oatt
 from attn_cases import BLOCK, error_stats, paged_cache, queries
@@ -55,23 +56,6 @@ def test_prefix_cache_chunks(device):
     out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
     ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
     _check(out, ref, "prefix-cache chunks")
-
-
-def mixed_step(seed, num_decode=48, k=4, num_chunks=3, budget=2048):
-    """A 2048-token-budget mixed step at Qwen3-8B shapes: decode requests (1+k verify rows, context lognormal
-    median 600, max 4096) first, then prefill chunks (length lognormal median 220, 0-512 cached prefix)."""
-    rnd = np.random.default_rng(seed)
-    dec_ctx = np.minimum(np.exp(rnd.normal(math.log(600), 0.6, num_decode)).astype(int) + k + 1, 4096).tolist()
-    left = budget - num_decode * (1 + k)
-    chunks = []
-    for _ in range(num_chunks):
-        L = int(min(max(np.exp(rnd.normal(math.log(220), 0.5)), 16), left))
-        left -= L
-        prefix = int(rnd.integers(0, 513))
-        chunks.append((L, prefix + L))
-    lq = [1 + k] * num_decode + [a for a, _ in chunks]
-    lk = dec_ctx + [b for _, b in chunks]
-    return lq, lk
 
 
 def test_mixed_step_vs_oracle_and_decode_rows_bitwise(device):

@@ -6,11 +6,13 @@ attention      textbook SDPA (float64, explicit boolean mask) over keys gathered
                decode on the same sequences; fresh rows == paged cache; empty context -> zeros.
 verify_drafts  the reference unit tests' known answers (tests/test_spec_unit.py:64-92), its zero-residual
                guard (:175-191) and TV-distance property (:137-172, including the deliberately wrong rule),
-               and golden vectors written by the reference's own sampler.py (tests/golden/).
+               and golden vectors written by the reference's own sampler.py (tests/golden/), at V = 512 and at
+               the full 151,936-token vocabulary.
 sample         closed form in float64 on tiny inputs; K = 0 verify equals sample.
 """
 import math
 import os
+import sys
 
 import numpy as np
 import pytest
@@ -21,6 +23,7 @@ from oracle import kvcache as okv
 from oracle import sampler as osmp
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "verify_vectors.npz")
+GOLDEN_FULL = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "verify_full_vocab.npz")
 
 
 # ------------------------------------------------------------------ store_kvcache
@@ -306,6 +309,22 @@ def test_verify_golden_vectors_from_reference():
                                   uniforms=c["uniforms"], exp_noise=c["noise"])
         assert a.tolist() == c["num_accepted"].tolist(), name
         assert t.tolist() == c["next_token"].tolist(), name
+
+
+@pytest.mark.parametrize("name", ["t0_f32_ngram", "t1_f32_draft", "t1_bf16_draft_ragged", "t005_f32_draft_masked",
+                                  "t01_bf16_ngram_masked", "mixed_f32_draft_ragged", "k0_f32_sample",
+                                  "zero_residual_t1_f32", "t0_bf16_draft_ragged", "t1_f32_ngram_ragged"])
+def test_verify_full_vocab_goldens_from_reference(name):
+    """Full-vocabulary outputs of the reference's sampler.py (inputs regenerated from seeds)."""
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import verify_inputs
+    data = np.load(GOLDEN_FULL)
+    c = verify_inputs.make_case(name)
+    assert verify_inputs.checksum(c) == str(data[f"{name}.checksum"])
+    logits, drafts, nd, temps, dl, u, e = c
+    a, t = osmp.verify_drafts(logits, drafts, nd, temps, dl, uniforms=u, exp_noise=e)
+    assert a.tolist() == data[f"{name}.num_accepted"].tolist()
+    assert t.tolist() == data[f"{name}.next_token"].tolist()
 
 
 # ------------------------------------------------------------------ sample
