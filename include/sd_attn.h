@@ -193,6 +193,23 @@ int sd_verify_drafts(const void* logits, int32_t logits_dtype, int64_t logits_ro
                      size_t workspace_bytes, void* stream);
 
 /*
+ * sd_verify_drafts without a workspace argument, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Same arguments, rule and results as sd_verify_drafts; the per-row statistics go to a scratch array of
+ * SD_VERIFY_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on until the process ends
+ * (looked up on the current device at its first call there). Calls that need more scratch than that
+ * (sd_verify_workspace_size of the same sizes) fail with SD_STATUS_UNSUPPORTED: about 1024 sequences x 15
+ * draft slots with draft logits fit. Every call on one GPU shares that GPU's scratch, so calls that overlap
+ * on one GPU (concurrent streams or threads) race; calls in one stream's order are safe.
+ */
+#define SD_VERIFY_NOALLOC_SCRATCH_BYTES (8u << 20)
+int sd_verify_drafts_noalloc(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                             const int64_t* draft_token_ids, const int64_t* num_drafts, const float* temperatures,
+                             const void* draft_logits, int32_t draft_dtype, int64_t draft_row_stride,
+                             const float* uniforms, const float* exp_noise, int32_t num_seqs, int32_t num_draft_slots,
+                             int32_t vocab, int64_t* num_accepted, int64_t* next_token, void* stream);
+
+/*
  * Inputs of one later draft step. Replaces the tensor operations of ModelRunner.run_draft's loop,
  * nanovllm/engine/model_runner.py:443-452 (steps j = 1 .. k-1). For every sequence b < num_seqs:
  *   real = real_lens[b] > 0 (the first draft step's context_lens; 0 marks a padding sequence)

@@ -21,6 +21,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "sd_common.h"
 #include "../../include/sd_attn.h"
@@ -664,6 +666,35 @@ int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_
   return launch_all<SD_DTYPE_BF16, SD_DTYPE_BF16, false>(p, s, draft);
 }
 
+// Scratch of the allocation-free entry point: one copy per GPU (a __device__ variable lives in every device's
+// code object), held until the process ends. Its host-side name is not a device address: kernels get the
+// address hipGetSymbolAddress returns on the current device, looked up once per device.
+constexpr size_t kStaticScratchBytes = SD_VERIFY_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+int static_scratch(const char* who, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(kLaunchFailed, "%s: no current device (or device index >= %d)", who, kMaxDevices);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (err != hipSuccess || !ptr)
+        return fail(kLaunchFailed, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                    hipGetErrorString(err));
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return kOk;
+}
+
 }  // namespace
 }  // namespace sd
 
@@ -699,4 +730,29 @@ extern "C" int sd_sample(const void* logits, int32_t logits_dtype, int64_t logit
   return run_verify("sd_sample", logits, logits_dtype, logits_row_stride, nullptr, nullptr, temperatures, nullptr,
                     SD_DTYPE_BF16, 0, nullptr, exp_noise, num_seqs, 0, vocab, scratch_a, next_token, workspace,
                     workspace_bytes, stream);
+}
+
+extern "C" int sd_verify_drafts_noalloc(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                                        const int64_t* draft_token_ids, const int64_t* num_drafts,
+                                        const float* temperatures, const void* draft_logits, int32_t draft_dtype,
+                                        int64_t draft_row_stride, const float* uniforms, const float* exp_noise,
+                                        int32_t num_seqs, int32_t num_draft_slots, int32_t vocab,
+                                        int64_t* num_accepted, int64_t* next_token, void* stream) {
+  const char* who = "sd_verify_drafts_noalloc";
+  if (!num_accepted) return fail(kBadArgument, "%s: null num_accepted", who);
+  if (num_seqs < 0 || num_draft_slots < 0 || num_draft_slots > 63 || vocab <= 0)
+    return fail(kBadArgument, "%s: bad sizes (seqs %d, draft slots %d (max 63), vocab %d)", who, num_seqs,
+                num_draft_slots, vocab);
+  if (num_seqs == 0) return kOk;
+  const size_t need = sd_verify_workspace_size(num_seqs, num_draft_slots, vocab, draft_logits != nullptr);
+  if (need > kStaticScratchBytes)
+    return fail(kUnsupported, "%s: %d sequences x %d slots need %zu B of scratch, more than the %zu B this entry "
+                "point holds; use sd_verify_drafts with a workspace", who, num_seqs, num_draft_slots, need,
+                kStaticScratchBytes);
+  void* ws = nullptr;
+  const int rc = static_scratch(who, &ws);
+  if (rc) return rc;
+  return run_verify(who, logits, logits_dtype, logits_row_stride, draft_token_ids, num_drafts, temperatures,
+                    draft_logits, draft_dtype, draft_row_stride, uniforms, exp_noise, num_seqs, num_draft_slots, vocab,
+                    num_accepted, next_token, ws, kStaticScratchBytes, stream);
 }

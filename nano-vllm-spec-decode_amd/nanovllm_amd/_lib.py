@@ -45,6 +45,9 @@ SIGNATURES = {
     "sd_verify_drafts": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64,
                                 _c_void_p, _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p, _c_void_p, _size,
                                 _c_void_p]),
+    "sd_verify_drafts_noalloc": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32,
+                                        _i64, _c_void_p, _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p,
+                                        _c_void_p]),
     "sd_draft_step_inputs": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _i32, _i32, _i32,
                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "sd_sample": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _c_void_p, _size,
