@@ -16,7 +16,9 @@ Also reported (same JSON line):
 * the rejection sampler (S 64, K 4, V 151936, T 0 and T 1 with draft logits);
 * the unfused path in front of it: the LM head as the library GEMM into bf16 logits, then the T 0 verifier;
 * a 2048-token mixed prefill+decode attention step over 36 layers, replayed as one HIP graph by the mixed-step
-  runtime (tok/s), and the prefill kernel at GPU-filling sizes;
+  runtime (tok/s), its roofline fractions, the prefill kernel at GPU-filling sizes, and the whole step of a
+  random-init Qwen3-8B-shaped model (36 layers run piecewise in the step's graph, then the LM head and the
+  verifier);
 * a CPU baseline: the oracle (PyTorch CPU restatement) timed on the headline workload for about 10 s on 16
   host threads.
 
@@ -32,7 +34,7 @@ import time
 import types
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-for _p in (ROOT, os.path.join(ROOT, "nano-vllm-spec-decode_amd"), os.path.join(ROOT, "tests")):
+for _p in (ROOT, os.path.join(ROOT, "nano-vllm-spec-decode_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
@@ -98,7 +100,7 @@ def graph_timed(fn, reps=20, replays=5):
 
 def bench_verify_attention(dev, steps, warmup, B=64, k=4, ctx_len=4096, W=33):
     import torch
-    from attn_cases import paged_cache, queries
+    from nanovllm_amd.engine.synthetic import paged_cache, queries
     from nanovllm_amd.layers.attention import paged_decode_attention
     n = k + 1
     ctx = [ctx_len] * B
@@ -119,7 +121,7 @@ def bench_verify_uniform(dev, B=64, k=4, lo=1024, hi=8192, W=33):
     import types
     import numpy as np
     import torch
-    from attn_cases import paged_cache, queries
+    from nanovllm_amd.engine.synthetic import paged_cache, queries
     from nanovllm_amd.layers.attention import paged_decode_attention
     n = k + 1
     ctx = np.random.default_rng(0).integers(lo, hi + 1, B).tolist()
@@ -150,7 +152,7 @@ def bench_verify_sweep(dev, ctx_len=4096, W=33):
     enough cache copies to exceed the 256 MB last-level cache."""
     import types
     import torch
-    from attn_cases import paged_cache, queries
+    from nanovllm_amd.engine.synthetic import paged_cache, queries
     from nanovllm_amd.layers.attention import paged_decode_attention
     res = {}
     for B in (64, 16, 1):  # the largest caches first, from a released allocator cache
@@ -289,8 +291,11 @@ def bench_draft_inputs(dev, B=64, W=33):
 
 
 def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
+    """The verifier through its C ABI (graph-timed): T 0 as the engine calls it when every row is greedy (no
+    temperatures, no noise: the argmax pass and the decision), and T 1 with draft logits and injected noise."""
     import torch
-    from nanovllm_amd.layers.sampler import verify_drafts
+    from nanovllm_amd import _lib
+    lib = _lib.load()
     g = torch.Generator(device=dev).manual_seed(4)
     logits = torch.randn(S * (K + 1), V, device=dev, generator=g) * 3
     dlog = torch.randn(S, K, V, device=dev, generator=g) * 3
@@ -298,13 +303,25 @@ def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
     nd = torch.full((S,), K, device=dev)
     u = torch.rand(S, K, device=dev, generator=g)
     e = torch.empty(S, V, device=dev).exponential_(1, generator=g)
+    acc = torch.empty(S, dtype=torch.int64, device=dev)
+    nxt = torch.empty(S, dtype=torch.int64, device=dev)
     res = {}
     for T, with_draft in ((0.0, False), (1.0, True)):
         temps = torch.full((S,), T, device=dev)
-        dl = dlog if with_draft else None
-        t = graph_timed(lambda: verify_drafts(logits, drafts, nd, temps, dl, uniforms=u, exp_noise=e), reps=10)
+        ws = torch.empty(lib.sd_verify_workspace_size(S, K, V, int(with_draft)), dtype=torch.uint8, device=dev)
+
+        def call():
+            _lib.check(lib.sd_verify_drafts(
+                logits.data_ptr(), _lib.DTYPE_F32, V, drafts.data_ptr(), nd.data_ptr(),
+                temps.data_ptr() if T else None, dlog.data_ptr() if with_draft else None, _lib.DTYPE_F32,
+                V if with_draft else 0, u.data_ptr() if T else None, e.data_ptr() if T else None, S, K, V,
+                acc.data_ptr(), nxt.data_ptr(), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream),
+                "sd_verify_drafts")
+        t = graph_timed(call, reps=10)
         nbytes = S * (K + 1) * V * 4 + ((S * K * V * 4 + 2 * S * V * 4 + S * V * 4) if T else 0)
-        res[f"T{int(T)}"] = dict(us=t * 1e6, GBs=nbytes / t / 1e9, bytes=nbytes, timing="graph replay of 10 calls")
+        res[f"T{int(T)}"] = dict(us=round(t * 1e6, 2), GBs=round(nbytes / t / 1e9, 1),
+                                 frac=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), bytes=nbytes,
+                                 timing="graph replay of 10 calls")
     return res
 
 
@@ -351,19 +368,19 @@ def bench_mixed_attention(dev, steps, warmup, layers=36):
     import numpy as np
     import torch
     from types import SimpleNamespace
-    from attn_cases import paged_cache, queries
+    from nanovllm_amd.engine.synthetic import paged_cache, queries
     from nanovllm_amd.engine.mixed_step import MixedStepRunner
     from nanovllm_amd.layers.attention import store_kvcache, varlen_attention
-    from test_gpu_mixed_step import K, _requests
-    from test_gpu_varlen import mixed_step
-    lq, lk = mixed_step(0)
+    from nanovllm_amd.engine.synthetic import mixed_step_lengths, requests
+    K = 4
+    lq, lk = mixed_step_lengths(0)
     nd = 48
     W = math.ceil(max(lk) / BLOCK)
     kc, vc, tables = paged_cache(dev, lk, HKV, D, W=W, seed=5)
     caches = [(kc, vc)] + [(torch.empty_like(kc).copy_(kc), torch.empty_like(vc).copy_(vc)) for _ in range(layers - 1)]
     runner = MixedStepRunner([SimpleNamespace(k_cache=a, v_cache=b) for a, b in caches], HQ, HKV, D, D ** -0.5,
                              block_size=BLOCK, max_num_batched_tokens=2048, max_num_seqs=64, table_width=W)
-    layout = runner.prepare(_requests(lq, lk, tables.cpu(), nd), K)
+    layout = runner.prepare(requests(lq, lk, tables.cpu(), nd, K, BLOCK), K)
     Nq, N = layout["n"], layout["N"]
     runner.bufs["q"][:N] = queries(dev, N, HQ, D, seed=6)
     runner.bufs["k"][:N] = queries(dev, N, HKV, D, seed=7)
@@ -423,7 +440,7 @@ def bench_prefill(dev):
     """The prefill q-block kernel on its own at sizes that fill the GPU (Qwen3-8B shapes, paged KV): 16
     chunks of 1024 queries after a 1024-token cached prefix, and one fresh 2048-token prompt. FLOPs are the
     causal attention's 4*Hq*D*(Lq*P + Lq(Lq+1)/2) per chunk."""
-    from attn_cases import paged_cache, queries
+    from nanovllm_amd.engine.synthetic import paged_cache, queries
     res = {}
     for name, lq, lk in (("16x1024_after_1024", [1024] * 16, [2048] * 16), ("1x2048", [2048], [2048])):
         kc, vc, tables = paged_cache(dev, lk, HKV, D, W=math.ceil(max(lk) / BLOCK), seed=21)
@@ -433,6 +450,68 @@ def bench_prefill(dev):
         res[name] = dict(us=round(t * 1e6, 2), tflops=round(flops / t / 1e12, 1),
                          mfma_frac=round(flops / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4))
         del kc, vc, tables, q
+    return res
+
+
+def bench_mixed_step_full(dev, layers=36, steps=5, warmup=2):
+    """The whole config-5 step: a random-init Qwen3-8B-shaped model (36 layers, hidden 4096, 32 q / 8 kv heads,
+    MLP 12288, vocab 151936, bf16) run piecewise by the mixed-step runtime in one HIP graph per bucket
+    (embedding, per layer: input norm + qkv GEMM, fused q/k norm + RoPE + KV store, varlen attention,
+    o_proj + post norm + MLP; final norm), then, eagerly as the reference's run_mixed does, the LM head on the
+    step's logits rows and the greedy verifier on the decode rows. Reports the model step alone (graph replay)
+    and the whole step, as query tokens per second."""
+    import torch
+    from types import SimpleNamespace
+    from nanovllm_amd import _lib
+    from nanovllm_amd.engine.mixed_step import MixedStepRunner
+    from nanovllm_amd.engine.qwen3_segments import Qwen3Segments
+    from nanovllm_amd.engine.synthetic import mixed_step_lengths, paged_cache, requests
+    K = 4
+    lq, lk = mixed_step_lengths(0)
+    nd = 48
+    W = math.ceil(max(lk) / BLOCK)
+    kc, vc, tables = paged_cache(dev, lk, HKV, D, W=W, seed=5)
+    caches = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(layers - 1)]
+    seg = Qwen3Segments(num_layers=layers, device=dev, seed=1)
+    runner = MixedStepRunner([SimpleNamespace(k_cache=a, v_cache=b) for a, b in caches], HQ, HKV, D, D ** -0.5,
+                             block_size=BLOCK, max_num_batched_tokens=2048, max_num_seqs=64, table_width=W,
+                             segment=seg, pre_attn=seg.pre_attn())
+    layout = runner.prepare(requests(lq, lk, tables.cpu(), nd, K, BLOCK), K)
+    n, N = layout["n"], layout["N"]
+    g = torch.Generator(device=dev).manual_seed(2)
+    seg.input_ids[:N] = torch.randint(0, 151936, (N,), device=dev, generator=g)
+    seg.input_ids[n:N] = 0
+    lib = _lib.load()
+    idx = torch.tensor(layout["logits_indices"], dtype=torch.int64, device=dev)
+    drafts = torch.randint(0, 151936, (nd, K), device=dev, generator=g)
+    ndr = torch.full((nd,), K, dtype=torch.int64, device=dev)
+    acc = torch.empty(nd, dtype=torch.int64, device=dev)
+    nxt = torch.empty(nd, dtype=torch.int64, device=dev)
+    V = 151936
+    ws = torch.empty(lib.sd_verify_workspace_size(nd, K, V, 0), dtype=torch.uint8, device=dev)
+
+    def model_step():
+        runner.run(layout)
+
+    def whole_step():
+        runner.run(layout)
+        logits = seg.logits(seg.hidden_out.index_select(0, idx))
+        _lib.check(lib.sd_verify_drafts(logits.data_ptr(), _lib.DTYPE_BF16, V, drafts.data_ptr(), ndr.data_ptr(),
+                                        None, None, 0, 0, None, None, nd, K, V, acc.data_ptr(), nxt.data_ptr(),
+                                        ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream),
+                   "sd_verify_drafts")
+
+    wall_m, _ = timed(model_step, steps, warmup)
+    wall_w, _ = timed(whole_step, steps, warmup)
+    gemm_flops = 2 * N * layers * (4096 * 6144 + 4096 * 4096 + 4096 * 24576 + 12288 * 4096)
+    res = dict(model_step_ms=round(wall_m * 1e3, 3), model_step_tok_s=round(n / wall_m, 1),
+               whole_step_ms=round(wall_w * 1e3, 3), whole_step_tok_s=round(n / wall_w, 1),
+               query_tokens=n, bucket_tokens=N, logits_rows=len(layout["logits_indices"]),
+               layer_gemm_tflops_per_step=round(gemm_flops / 1e12, 2),
+               timing="wall clock of back-to-back steps between synchronizations (the step's metadata copy, "
+                      "one graph replay, then the LM head and the verifier eagerly)")
+    del caches, kc, vc, seg, runner
+    torch.cuda.empty_cache()
     return res
 
 
@@ -476,7 +555,8 @@ def cpu_baseline(inputs, min_seconds=10.0, max_reps=8):
     import torch
     from oracle import attention as oatt
     q, kc, vc, lens, tables = inputs
-    torch.set_num_threads(min(16, os.cpu_count() or 1))   # at most 16 host threads per GPU
+    # at most 16 host threads: the CPU share of one GPU on a shared 8-GPU host, whatever os.cpu_count() says
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
     qs, ls, ts = q.cpu(), lens.cpu(), tables.cpu()
     kcs, vcs = kc.cpu(), vc.cpu()
     oatt.paged_decode_attention(qs[:2], kcs, vcs, ls[:2], ts[:2], D ** -0.5)
@@ -489,9 +569,21 @@ def cpu_baseline(inputs, min_seconds=10.0, max_reps=8):
     t = total / reps
     nbytes = decode_bytes(ls.tolist(), q.size(1))
     return dict(value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(), kind="port",
+                cpu_model=cpu_model(), os_cpu_count=os.cpu_count(),
+                threads_note="16 threads: the host-core share of one GPU on the 8-GPU host, not all cores",
                 sample=f"the full headline call (64 sequences, ctx 4096, k=4) through the oracle's "
                        f"paged_decode_attention, {reps} runs, {total:.1f} s total, {t * 1e3:.0f} ms per call",
                 secondary=cpu_secondary())
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_secondary(reps=3):
@@ -506,7 +598,7 @@ def cpu_secondary(reps=3):
     from oracle import kvcache as okv
     from oracle import qk_norm_rope as onr
     from oracle import sampler as osmp
-    from test_gpu_varlen import mixed_step
+    from nanovllm_amd.engine.synthetic import mixed_step_lengths
     g = torch.Generator().manual_seed(7)
     N, NB, W = 2048, 512, 33
     qkv = torch.randn(N, (HQ + 2 * HKV) * D, generator=g).to(torch.bfloat16)
@@ -547,7 +639,7 @@ def cpu_secondary(reps=3):
         clock(f"verify_T{int(T)}_ms", lambda: osmp.verify_drafts(logits, drafts, nd, torch.full((S,), T),
                                                                  dlog if T else None, uniforms=u, exp_noise=e), 1)
     del logits, dlog, e
-    lq, lk = mixed_step(0)
+    lq, lk = mixed_step_lengths(0)
     Wm = math.ceil(max(lk) / BLOCK)
     nblk = sum(math.ceil(c / BLOCK) for c in lk)
     kcm = torch.randn(nblk, BLOCK, HKV, D, generator=g).to(torch.bfloat16)
@@ -584,7 +676,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-extras", action="store_true", help="headline only (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="leave out the CPU baseline (for profiling)")
-    ap.add_argument("--only", choices=["qk_norm_rope_store", "draft_step_inputs", "kv_store", "lm_head_verify"],
+    ap.add_argument("--only", choices=["qk_norm_rope_store", "draft_step_inputs", "kv_store", "lm_head_verify",
+                                       "verify_sampler", "mixed_step_full", "mixed_step_attention", "prefill_kernel"],
                     help="run one secondary workload alone and print its JSON (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
@@ -605,7 +698,11 @@ def main():
     if args.only:
         fn = {"qk_norm_rope_store": lambda: bench_qk_norm_rope(dev), "draft_step_inputs": lambda: bench_draft_inputs(dev),
               "kv_store": lambda: bench_store(dev, args.steps, args.warmup),
-              "lm_head_verify": lambda: bench_lm_head_verify(dev)}[args.only]
+              "lm_head_verify": lambda: bench_lm_head_verify(dev),
+              "verify_sampler": lambda: bench_sampler(dev, args.steps, args.warmup),
+              "mixed_step_full": lambda: bench_mixed_step_full(dev),
+              "mixed_step_attention": lambda: bench_mixed_attention(dev, max(5, args.steps // 10), 2),
+              "prefill_kernel": lambda: bench_prefill(dev)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
     head = bench_verify_attention(dev, args.steps, args.warmup)
@@ -631,7 +728,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
                      "kernel": "attn_fwd<RT=2, 8 waves> (one sd_paged_decode call: one launch, residues merged in LDS)",
-                     "bytes_per_launch": head["bytes"], "us_per_launch": round(t * 1e6, 2)},
+                     "bytes_per_launch": head["bytes"], "us_per_launch": round(t * 1e6, 2),
+                     "timing": "mean of per-launch HIP event pairs on the launch stream over the timed steps "
+                               "(rocprofv3 kernel average: profiles/bench_workloads.kernel_stats.txt)"},
     }
     if not args.skip_extras:
         result["verify_attention_uniform_ctx"] = bench_verify_uniform(dev)
@@ -643,6 +742,19 @@ def main():
         result["lm_head_then_verify"] = bench_lm_head_verify(dev)
         mixed = bench_mixed_attention(dev, max(5, args.steps // 10), 2)
         result["mixed_step_attention"] = mixed
+        layer_s = mixed["layer_attention_us"] / 1e6
+        pre_tf = mixed["prefill_flops_per_layer"] / 1e12
+        result["mixed_step_roofline"] = {
+            "bound": "mfma (prefill rows) + hbm (decode rows)",
+            "prefill_achieved_tflops": round(pre_tf / layer_s, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+            "prefill_frac_of_layer_time": round(pre_tf / layer_s / MFMA_BF16_PEAK_TFLOPS, 4),
+            "decode_achieved_GBs": round(mixed["decode_bytes_per_layer"] / layer_s / 1e9, 1),
+            "decode_frac_of_layer_time": round(mixed["decode_bytes_per_layer"] / layer_s / 1e9 / HBM_PEAK_GBS, 4),
+            "combined_frac": round((pre_tf / MFMA_BF16_PEAK_TFLOPS
+                                    + mixed["decode_bytes_per_layer"] / (HBM_PEAK_GBS * 1e9)) / layer_s, 4),
+            "note": "one layer's attention launch (planned work lists, caches cycled over 36 layers); combined_frac "
+                    "= (prefill FLOPs / MFMA peak + decode bytes / HBM peak) / layer time"}
+        result["mixed_step_full_model"] = bench_mixed_step_full(dev)
         result["prefill_kernel"] = bench_prefill(dev)
     if not args.skip_extras and not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(head["inputs"])

@@ -1,21 +1,23 @@
 // Speculative-decoding verifier and token sampler over the full vocabulary (replaces verify_drafts and
 // Sampler.forward, nanovllm/layers/sampler.py:5-103).
 //
-// Four kernels, two of them HBM-streaming over [rows, vocab] tables. A row is cut into at most
-// kSpans contiguous spans (a multiple of 4 entries each, none empty); a 256-thread workgroup streams one
-// span with 4-entry loads (16 B for fp32, 8 B for bf16; scalar loads when the rows are not aligned).
-//   1. row_stats      (row, span): first argmax of the raw logits of target rows; for rows with temperature
-//                     != 0 also max and sum(exp(x - max)) of x = l / T (target rows and, when given, draft
-//                     rows), kept per thread online and combined in a fixed order.
-//   2. verify_decide  (seq): merges span stats in span order (argmax, logsumexp), applies the accept rule
-//                     u * q(d) < p(d) (or top1 == d for greedy rows) to the leading run of real guesses,
-//                     writes num_accepted and, for greedy rows, next_token.
-//   3. verify_resample(seq, span): random rows only, over up to 64 spans per row (a single row per
-//                     sequence: more spans keep a small batch spread over the GPU): the first argmax of
-//                     p / max(E, 1e-10) and of
-//                     residual / max(E, 1e-10) with p = softmax(row a / T), residual = max(p - q, 0) (or p
-//                     with the rejected n-gram guess zeroed), and whether any residual is positive.
-//   4. verify_finish  (seq): random rows only: merges the span candidates and picks the token.
+// Two HBM-streaming kernels over [rows, vocab] tables and two small ones. A row is cut into at most kSpans
+// contiguous spans (a multiple of 4 entries each, none empty); a 256-thread workgroup streams one span with
+// 4-entry loads (16 B for fp32, 8 B for bf16; scalar loads when the rows are not aligned).
+//   1. row_stats       (row, span): first argmax of the raw logits of target rows; for rows with temperature
+//                      != 0 also max and sum(exp(x - max)) of x = l / T (target rows and, when given, draft
+//                      rows), kept per thread online and combined in a fixed order.
+//   decide_seq         (seq): merges span stats in span order (argmax, logsumexp), applies the accept rule
+//                      u * q(d) < p(d) (or top1 == d for greedy rows) to the leading run of real guesses,
+//                      writes num_accepted and, for greedy rows, next_token. It runs as its own kernel
+//                      (verify_decide) when every row is greedy, else in the prologue of every resample
+//                      workgroup of the sequence.
+//   2. verify_resample (seq, span): random rows only, over up to 64 spans per row (a single row per
+//                      sequence: more spans keep a small batch spread over the GPU): the first argmax of
+//                      p / max(E, 1e-10) and of residual / max(E, 1e-10) with p = softmax(row a / T), residual =
+//                      max(p - q, 0) (or p with the rejected n-gram guess zeroed), and whether any residual is
+//                      positive; exact values only for the entries that bounds cannot rule out.
+//   3. verify_finish   (seq): random rows only: merges the span candidates and picks the token.
 // Every reduction has a fixed order, so results are deterministic; ties resolve to the first index (and a
 // NaN counts as the largest value), as torch.argmax does.
 #include <math.h>
@@ -98,22 +100,59 @@ __device__ __forceinline__ float exp_acc(float x) {
   return ldexpf(__builtin_amdgcn_exp2f(f), (int)n);
 }
 
+// exp(x) for the terms of the streaming sums: v_exp_f32 (0.77 ulp over its whole range) of the rounded
+// product t = x*log2(e), corrected by that product's rounding error with one fma: within 1.25 ulp of e^x for
+// normal results (measured on 4M inputs in [-120, 5]); results below 2^-126 flush to 0, which no sum that holds
+// a term exp(0) = 1 can see. x = -inf gives 0 (clamped to -104 first), NaN stays NaN.
+__device__ __forceinline__ float exp_term(float x) {
+#pragma clang fp contract(off)
+  x = x < -104.f ? -104.f : x;
+  const float kHi = 1.44269502162933349609375f;
+  const float kLo = 1.925963033500011e-08f;
+  const float t = x * kHi;
+  const float err = fmaf(x, kLo, fmaf(x, kHi, -t));
+  const float r = __builtin_amdgcn_exp2f(t);
+  return fmaf(r, err * 0.693147180559945309f, r);
+}
+
+// x / T with z = 1/T correctly rounded (one division per workgroup): y = x*z lies within an ulp of the
+// quotient, its residual x - y*T is exact (fma), and one correction step gives the correctly rounded quotient
+// (Markstein's theorem; checked against IEEE division on 2.8e9 random fp32 x in [2^-100, 2^100] for 18
+// temperatures from 0.01 to 3). Infinite x keeps its sign; tiny x may be an ulp off, which no sum of
+// exponentials sees. Used by the streaming passes only; the decisions divide.
+__device__ __forceinline__ float div_by(float x, float T, float z) {
+#pragma clang fp contract(off)
+  const float y = x * z;
+  return __builtin_isinf(y) ? y : fmaf(fmaf(-y, T, x), z, y);
+}
+
 // The shift of a logsumexp: the maximum, or 0 when it is infinite (torch.logsumexp's rule), so that
 // an all -inf set sums to 0 (lse -inf) and a +inf entry gives +inf.
 __device__ __forceinline__ float lse_shift(float m) { return fabsf(m) == INFINITY ? 0.f : m; }
 
 // Online (max m, sum s of exp(x - lse_shift(m))) of one thread's entries. s == 0 exactly while every entry
-// seen is -inf; a rescale is skipped then (it would multiply 0 by an overflowing factor).
+// seen is -inf; a rescale leaves it 0 then (it would multiply 0 by an overflowing factor). A +inf entry makes
+// the sum +inf (finish()).
 struct OnlineSum {
   float m = -INFINITY, s = 0.f;
-  __device__ __forceinline__ void add4(float x0, float x1, float x2, float x3) {
-    const float ml = fmaxf(fmaxf(x0, x1), fmaxf(x2, x3));
-    if (ml > m) {
-      if (s != 0.f) s *= exp_acc(lse_shift(m) - lse_shift(ml));
-      m = ml;
-    }
+  // Adds N entries: one rescale to their common max, then N exponentials.
+  template <int N>
+  __device__ __forceinline__ void add(const float (&x)[N]) {
+    float ml = x[0];
+#pragma unroll
+    for (int e = 1; e < N; ++e) ml = fmaxf(ml, x[e]);
+    const float mn = fmaxf(m, ml);
+    const float f = exp_term(lse_shift(m) - lse_shift(mn));
+    s = s != 0.f ? s * f : 0.f;
+    m = mn;
     const float sh = lse_shift(m);
-    s += exp_acc(x0 - sh) + exp_acc(x1 - sh) + exp_acc(x2 - sh) + exp_acc(x3 - sh);
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < N; ++e) acc += exp_term(x[e] - sh);
+    s += acc;
+  }
+  __device__ __forceinline__ void finish() {
+    if (m == INFINITY) s = INFINITY;
   }
 };
 
@@ -207,6 +246,63 @@ struct VParams {
   Cand* cand;                     // [S][rchunk]
 };
 
+// One span of one row: the first argmax of the raw values (kArg) and the online (max, sum) of x = value / T
+// (kSum; kDiv when T != 1). A thread visits v0 + 4*tid, then every 4*kThreads entries, in increasing order;
+// the aligned main loop has four of those 4-entry loads in flight and folds their 16 entries into the sum with
+// one rescale. Within a thread indices only grow, so a later entry replaces the argmax only when larger (or
+// NaN over a non-NaN), which is torch.argmax's first-index rule.
+template <int DTX, bool kVec, bool kArg, bool kSum, bool kDiv>
+__device__ __forceinline__ void scan_span(const void* base, int v0, int v1, float T, float z, float& bv, int& bi,
+                                          OnlineSum& os) {
+  auto arg = [&](float r, int v) {
+    if (bv == bv && !(r <= bv)) {
+      bv = r;
+      bi = v;
+    }
+  };
+  auto xof = [&](float r) { return kDiv ? div_by(r, T, z) : r; };
+  constexpr int kStep = 4 * kThreads;
+  int v = v0 + 4 * threadIdx.x;
+  if (kVec) {
+    for (; v + 3 * kStep + 4 <= v1; v += 4 * kStep) {
+      float4 q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) q[u] = load_logit4<DTX>(base, v + u * kStep);
+      float x[16];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float r[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (kArg) arg(r[e], v + u * kStep + e);
+          x[4 * u + e] = xof(r[e]);
+        }
+      }
+      if (kSum) os.add(x);
+    }
+  }
+  for (; v < v1; v += kStep) {
+    float r[4];
+    if (kVec && v + 4 <= v1) {
+      const float4 q4 = load_logit4<DTX>(base, v);
+      r[0] = q4.x, r[1] = q4.y, r[2] = q4.z, r[3] = q4.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = v + e < v1 ? load_logit<DTX>(base, v + e) : -INFINITY;
+    }
+    float x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (kArg && v + e < v1) arg(r[e], v + e);
+      x[e] = v + e < v1 ? xof(r[e]) : -INFINITY;
+    }
+    if (kSum) os.add(x);
+  }
+}
+
+// Grid (rows, spans): target rows first (argmax; with a temperature also the softmax statistics of l / T),
+// then the draft rows of sampled sequences (statistics only). Each workgroup takes one uniform branch to the
+// scan it needs.
 template <int DT, int DDT, bool kVec, bool kRand>
 __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
   __shared__ float shf[8];
@@ -219,70 +315,30 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
   const float T = kRand ? p.temps[seq] : 0.f;
   const bool random = kRand && T != 0.f;
   if (!is_target && !random) return;  // draft rows only matter for sampled rows
-  const void* base;
-  if (is_target) {
-    base = DT == SD_DTYPE_F32 ? (const void*)((const float*)p.logits + (int64_t)row * p.logits_stride)
-                              : (const void*)((const uint16_t*)p.logits + (int64_t)row * p.logits_stride);
-  } else {
-    const int64_t dr = row - target_rows;
-    base = DDT == SD_DTYPE_F32 ? (const void*)((const float*)p.draft_logits + dr * p.draft_stride)
-                               : (const void*)((const uint16_t*)p.draft_logits + dr * p.draft_stride);
-  }
   const int v0 = chunk * p.span;
   const int v1 = min(v0 + p.span, p.V);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   OnlineSum os;
-  auto visit = [&](float raw, int v) {  // scalar entry
-    if (is_target && better(raw, v, bv, bi)) {
-      bv = raw;
-      bi = v;
-    }
-  };
-  auto load4 = [&](int v) {
-    return is_target ? load_logit4<DT>(base, v) : load_logit4<DDT>(base, v);
-  };
-  auto body = [&](int v, const float (&r)[4]) {  // entries v .. v+3 (those below v1)
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (v + e < v1) visit(r[e], v + e);
-    if (random) {
-      float x[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = v + e < v1 ? (T == 1.f ? r[e] : r[e] / T) : -INFINITY;  // x / 1 == x
-      os.add4(x[0], x[1], x[2], x[3]);
-    }
-  };
-  // A thread visits v0 + 4*tid, then every 4*kThreads entries, in increasing order; the aligned main loop
-  // issues four of those loads before using any (the same visiting order, more loads in flight).
-  constexpr int kStep = 4 * kThreads;
-  int v = v0 + 4 * threadIdx.x;
-  if (kVec) {
-    for (; v + 3 * kStep + 4 <= v1; v += 4 * kStep) {
-      float4 q[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) q[u] = load4(v + u * kStep);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float r[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
-        body(v + u * kStep, r);
-      }
-    }
-  }
-  for (; v < v1; v += kStep) {
-    float r[4];
-    if (kVec && v + 4 <= v1) {
-      const float4 q4 = load4(v);
-      r[0] = q4.x;
-      r[1] = q4.y;
-      r[2] = q4.z;
-      r[3] = q4.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        r[e] = v + e < v1 ? (is_target ? load_logit<DT>(base, v + e) : load_logit<DDT>(base, v + e)) : -INFINITY;
-    }
-    body(v, r);
+  const float z = random ? 1.f / T : 1.f;
+  if (is_target) {
+    const void* base = DT == SD_DTYPE_F32
+                           ? (const void*)((const float*)p.logits + (int64_t)row * p.logits_stride)
+                           : (const void*)((const uint16_t*)p.logits + (int64_t)row * p.logits_stride);
+    if (!random)
+      scan_span<DT, kVec, true, false, false>(base, v0, v1, T, z, bv, bi, os);
+    else if (T == 1.f)
+      scan_span<DT, kVec, true, true, false>(base, v0, v1, T, z, bv, bi, os);
+    else
+      scan_span<DT, kVec, true, true, true>(base, v0, v1, T, z, bv, bi, os);
+  } else {
+    const int64_t dr = row - target_rows;
+    const void* base = DDT == SD_DTYPE_F32 ? (const void*)((const float*)p.draft_logits + dr * p.draft_stride)
+                                           : (const void*)((const uint16_t*)p.draft_logits + dr * p.draft_stride);
+    if (T == 1.f)
+      scan_span<DDT, kVec, false, true, false>(base, v0, v1, T, z, bv, bi, os);
+    else
+      scan_span<DDT, kVec, false, true, true>(base, v0, v1, T, z, bv, bi, os);
   }
   RowStat st;
   st.max_x = -INFINITY;
@@ -291,6 +347,7 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
   st.best = bv;
   st.best_idx = bi;
   if (random) {
+    os.finish();
     combine_online(os, shf);
     st.max_x = os.m;
     st.sum = os.s;
@@ -312,98 +369,122 @@ __device__ void merge_softmax(const RowStat* st, int nchunk, float* shift_out, f
   *S_out = s;
 }
 
+// The decision for one sequence, by one workgroup (any size from 64 threads; every thread must call it). Every
+// global read is issued up front (the span statistics of the sequence's rows into LDS; per guess slot the guess,
+// its uniform and its target and draft logits), then lane j merges row j's spans and evaluates guess j, and the
+// leading run of accepts gives a. With `publish`, thread 0 writes num_accepted, the greedy token and the
+// sequence's SeqInfo. Returns that SeqInfo to every thread.
 template <int DT, int DDT, bool kRand>
-__global__ __launch_bounds__(64) void verify_decide(VParams p) {
-  __shared__ int32_t top1[65];
-  __shared__ float lse[65];
-  __shared__ float dlse[64];
-  const int seq = blockIdx.x;
+__device__ SeqInfo decide_seq(const VParams& p, int seq, bool publish) {
+  __shared__ RowStat sst[(64 + 63) * kSpans];
+  __shared__ int32_t top1[64];
+  __shared__ float lse[64], dlse[64], tshift[64], tsum[64], dshift[64], dsum[64];
+  __shared__ int accj[64];
+  __shared__ int64_t guess[64];
+  __shared__ SeqInfo shared_info;
   const int lane = threadIdx.x;
-  const int K = p.K;
+  const int nthr = blockDim.x;
+  const int K = p.K, nchunk = p.nchunk;
   const float T = kRand ? p.temps[seq] : 0.f;
   const bool random = kRand && T != 0.f;
+  const bool draft = random && p.draft_logits;
   const int target_rows = p.S * (K + 1);
-  for (int j = lane; j <= K; j += 64) {
-    const RowStat* st = p.stats + (int64_t)(seq * (K + 1) + j) * p.nchunk;
+  const int nt = (K + 1) * nchunk, nd_stats = draft ? K * nchunk : 0;
+  const RowStat* tst = p.stats + (int64_t)seq * (K + 1) * nchunk;
+  const RowStat* dst = p.stats + ((int64_t)target_rows + (int64_t)seq * K) * nchunk;
+  for (int i = lane; i < nt; i += nthr) sst[i] = tst[i];
+  for (int i = lane; i < nd_stats; i += nthr) sst[nt + i] = dst[i];
+  const int64_t nd = p.num_drafts ? p.num_drafts[seq] : 0;
+  int64_t d = -1;
+  float xl = 0.f, xd = 0.f, u = 1.f;
+  if (lane < K) {
+    d = guess[lane] = p.drafts[(int64_t)seq * K + lane];
+    if (random && d >= 0 && d < p.V) {
+      const int64_t trow = (int64_t)seq * (K + 1) + lane;
+      xl = DT == SD_DTYPE_F32 ? ((const float*)p.logits)[trow * p.logits_stride + d]
+                              : bf16_bits_to_f32(((const uint16_t*)p.logits)[trow * p.logits_stride + d]);
+      if (draft) {
+        const int64_t dr = (int64_t)seq * K + lane;
+        xd = DDT == SD_DTYPE_F32 ? ((const float*)p.draft_logits)[dr * p.draft_stride + d]
+                                 : bf16_bits_to_f32(((const uint16_t*)p.draft_logits)[dr * p.draft_stride + d]);
+      }
+      if (p.uniforms) u = p.uniforms[(int64_t)seq * K + lane];  // missing uniforms: u = 1
+    }
+  }
+  __syncthreads();
+  if (lane <= K) {
+    const RowStat* st = sst + lane * nchunk;
     float bv = st[0].best;
     int bi = st[0].best_idx;
-    for (int c = 1; c < p.nchunk; ++c)
+    for (int c = 1; c < nchunk; ++c)
       if (better(st[c].best, st[c].best_idx, bv, bi)) {
         bv = st[c].best;
         bi = st[c].best_idx;
       }
-    top1[j] = bi;
+    top1[lane] = bi;
     if (random) {
-      float M, s;
-      merge_softmax(st, p.nchunk, &M, &s);
-      lse[j] = logf(s) + M;
+      merge_softmax(st, nchunk, &tshift[lane], &tsum[lane]);
+      lse[lane] = logf(tsum[lane]) + tshift[lane];
     }
   }
-  if (random && p.draft_logits) {
-    for (int j = lane; j < K; j += 64) {
-      const RowStat* st = p.stats + (int64_t)(target_rows + seq * K + j) * p.nchunk;
-      float M, s;
-      merge_softmax(st, p.nchunk, &M, &s);
-      dlse[j] = logf(s) + M;
-    }
+  if (draft && lane < K) {
+    merge_softmax(sst + nt + lane * nchunk, nchunk, &dshift[lane], &dsum[lane]);
+    dlse[lane] = logf(dsum[lane]) + dshift[lane];
   }
   __syncthreads();
-  // Each lane evaluates one guess (the scattered loads run in parallel), lane 0 takes the leading run.
-  __shared__ int accj[64];
-  const int64_t nd = p.num_drafts ? p.num_drafts[seq] : 0;
-  for (int j = lane; j < K; j += 64) {
-    const int64_t d = p.drafts[(int64_t)seq * K + j];
+  if (lane < K) {
     bool acc = false;
-    if (j < nd && d >= 0 && d < p.V) {
+    if (lane < nd && d >= 0 && d < p.V) {
       if (!random) {
-        acc = top1[j] == d;
+        acc = top1[lane] == d;
       } else {
-        const float xl = (DT == SD_DTYPE_F32)
-                             ? ((const float*)p.logits)[(int64_t)(seq * (K + 1) + j) * p.logits_stride + d]
-                             : bf16_bits_to_f32(((const uint16_t*)p.logits)[(int64_t)(seq * (K + 1) + j) * p.logits_stride + d]);
-        const float pd = exp_acc(xl / T - lse[j]);
-        float qd = 1.f;
-        if (p.draft_logits) {
-          const int64_t dr = (int64_t)seq * K + j;
-          const float xd = (DDT == SD_DTYPE_F32)
-                               ? ((const float*)p.draft_logits)[dr * p.draft_stride + d]
-                               : bf16_bits_to_f32(((const uint16_t*)p.draft_logits)[dr * p.draft_stride + d]);
-          qd = exp_acc(xd / T - dlse[j]);
-        }
-        const float u = p.uniforms ? p.uniforms[(int64_t)seq * K + j] : 1.f;  // missing uniforms: u = 1
+        const float pd = exp_acc(xl / T - lse[lane]);
+        const float qd = draft ? exp_acc(xd / T - dlse[lane]) : 1.f;
         acc = u * qd < pd;
       }
     }
-    accj[j] = acc ? 1 : 0;
+    accj[lane] = acc ? 1 : 0;
   }
   __syncthreads();
-  if (lane != 0) return;
-  int a = 0;
-  while (a < K && accj[a]) ++a;
-  p.out_a[seq] = a;
-  SeqInfo info{};
-  info.a = a;
-  info.random = random ? 1 : 0;
-  info.guess = -1;
-  if (!random) {
-    p.out_next[seq] = top1[a];
-  } else {
-    const RowStat* st = p.stats + (int64_t)(seq * (K + 1) + a) * p.nchunk;
-    merge_softmax(st, p.nchunk, &info.Ma, &info.Sa);
-    info.rejected = a < nd ? 1 : 0;
-    if (K > 0) {
-      const int j = min(a, K - 1);
-      const int64_t d = p.drafts[(int64_t)seq * K + j];
-      if (p.draft_logits) {
-        info.resid_mode = 2;
-        merge_softmax(p.stats + (int64_t)(target_rows + seq * K + j) * p.nchunk, p.nchunk, &info.Md, &info.Sd);
-      } else {
-        info.resid_mode = 1;
-        info.guess = (d >= 0 && d < p.V) ? (int32_t)d : -1;
+  if (lane == 0) {
+    int a = 0;
+    while (a < K && accj[a]) ++a;
+    SeqInfo info{};
+    info.a = a;
+    info.random = random ? 1 : 0;
+    info.guess = -1;
+    if (random) {
+      info.Ma = tshift[a];
+      info.Sa = tsum[a];
+      info.rejected = a < nd ? 1 : 0;
+      if (K > 0) {
+        const int j = min(a, K - 1);
+        if (draft) {
+          info.resid_mode = 2;
+          info.Md = dshift[j];
+          info.Sd = dsum[j];
+        } else {
+          info.resid_mode = 1;
+          const int64_t dj = guess[j];
+          info.guess = (dj >= 0 && dj < p.V) ? (int32_t)dj : -1;
+        }
       }
     }
+    shared_info = info;
+    if (publish) {
+      p.out_a[seq] = a;
+      if (!random) p.out_next[seq] = top1[a];
+      p.info[seq] = info;
+    }
   }
-  p.info[seq] = info;
+  __syncthreads();
+  return shared_info;
+}
+
+// The decision alone, one 64-lane workgroup per sequence (the all-greedy path, where no resampling follows).
+template <int DT, int DDT, bool kRand>
+__global__ __launch_bounds__(64) void verify_decide(VParams p) {
+  decide_seq<DT, DDT, kRand>(p, blockIdx.x, true);
 }
 
 // One workgroup per random sequence: thread k reads span k's candidate (all reads in flight together),
@@ -438,106 +519,188 @@ __global__ __launch_bounds__(kThreads) void verify_finish(VParams p) {
   if (threadIdx.x == 0) p.out_next[seq] = use_res ? ri : pi;
 }
 
+// verify_resample streams its span with approximate values and computes exact ones only where they can matter.
+// The exact values are the reference's: prob = exp(x - shift) / sum with x = l / T, p / max(E, 1e-10) and
+// max(prob - q, 0) / max(E, 1e-10), each an IEEE division of exp_acc results. The approximations replace the
+// divisions by products with reciprocals and the exponential by one v_exp_f32; for every entry whose prob is a
+// normal number they are within eps = (|shift| + 323) * 2^-22 of the exact values (x = l / T within 1.5 * 2^-23 |x|,
+// the subtraction and the product with log2(e) 2^-24 of |x - shift| each, v_exp_f32 1 ulp, reciprocals and
+// products a few ulps; |x - shift| <= 104.5 wherever exp_acc does not underflow to 0). So each entry has a lower
+// bound lb <= exact <= ub, and with L the largest lower bound of the span, the winner (and every entry tied with
+// it) has ub >= L. A lane keeps the entry with the largest ub and the second-largest ub; when that second is below
+// L, its only entry that can reach L is the first, which is computed exactly. Otherwise (and whenever the bounds
+// are not trusted: L below 2^-60, where flushed approximations of exact values up to 2^-126 / 1e-10 may hide, a
+// NaN, or no residual sure to be positive) the lane reads its entries again and computes exactly each one that
+// may reach L (every one with a possibly non-zero prob in the untrusted cases). The exact argmax (ties: the
+// lower index) of the computed entries is then the argmax over all entries.
+constexpr float kTinyBest = 8.673617379884035e-19f;  // 2^-60
+constexpr float kUnderflow = -104.5f;
+
 template <int DT, int DDT, bool kVec>
 __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
-  __shared__ float shf[4];
+  __shared__ float shf[8];
   __shared__ int shi[4];
   const int seq = blockIdx.x;
   const int chunk = blockIdx.y;
-  const SeqInfo info = p.info[seq];
+  // Every span's workgroup takes the sequence's decision itself (the statistics are a few KB); span 0's
+  // publishes it.
+  const SeqInfo info = decide_seq<DT, DDT, true>(p, seq, chunk == 0);
   if (!info.random) return;
   const float T = p.temps[seq];
+  const bool div = T != 1.f;
+  const float z = 1.f / T;
   const int K = p.K;
   const int64_t trow = (int64_t)seq * (K + 1) + info.a;
   const int64_t drow = (int64_t)seq * K + min(info.a, K - 1);
   const void* tbase = DT == SD_DTYPE_F32 ? (const void*)((const float*)p.logits + trow * p.logits_stride)
                                          : (const void*)((const uint16_t*)p.logits + trow * p.logits_stride);
+  const bool resid = info.resid_mode == 2;
   const void* dbase = nullptr;
-  if (info.resid_mode == 2)
+  if (resid)
     dbase = DDT == SD_DTYPE_F32 ? (const void*)((const float*)p.draft_logits + drow * p.draft_stride)
                                 : (const void*)((const uint16_t*)p.draft_logits + drow * p.draft_stride);
   const float* noise = p.noise ? p.noise + (int64_t)seq * p.V : nullptr;  // missing noise: E = 1
+  const int zap = info.resid_mode == 1 && info.rejected ? info.guess : -1;  // n-gram: prob of the guess is 0
+  const float kL2E = 1.4426950408889634f;
+  const float invSa = 1.f / info.Sa, invSd = resid ? 1.f / info.Sd : 0.f;
+  const float eps = (fmaxf(fabsf(info.Ma), resid ? fabsf(info.Md) : 0.f) + 323.f) * 2.384185791015625e-07f;
+  const float up = 1.f + 2.f * eps, dn = 1.f - 2.f * eps;
   const int v0 = chunk * p.rspan;
   const int v1 = min(v0 + p.rspan, p.V);
   float pv = -INFINITY, rv = -INFINITY;
   int pi = 0x7fffffff, ri = 0x7fffffff;
   int any_res = 0;
-  auto body = [&](int v, const float (&l)[4], const float (&E)[4], const float (&ld)[4]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int idx = v + e;
-      if (idx >= v1) continue;
-      float prob = exp_acc((T == 1.f ? l[e] : l[e] / T) - info.Ma) / info.Sa;
-      const float Ee = noise ? fmaxf(E[e], 1e-10f) : 1.f;
-      if (info.resid_mode == 1 && info.rejected && idx == info.guess) prob = 0.f;
-      const float sp = prob / Ee;
-      if (better(sp, idx, pv, pi)) {
-        pv = sp;
-        pi = idx;
+  // Exact values of entry i, folded into the lane's bests.
+  auto exact = [&](int i, float l, float E, float ld) {
+    float prob = exp_acc((div ? l / T : l) - info.Ma) / info.Sa;
+    const float Ee = noise ? fmaxf(E, 1e-10f) : 1.f;
+    if (i == zap) prob = 0.f;
+    const float sp = prob / Ee;
+    if (better(sp, i, pv, pi)) {
+      pv = sp;
+      pi = i;
+    }
+    if (resid) {
+      const float q = exp_acc((div ? ld / T : ld) - info.Md) / info.Sd;
+      const float res = fmaxf(prob - q, 0.f);
+      any_res |= res > 0.f;
+      const float sr = res / Ee;
+      if (better(sr, i, rv, ri)) {
+        rv = sr;
+        ri = i;
       }
-      if (dbase) {
-        const float q = exp_acc((T == 1.f ? ld[e] : ld[e] / T) - info.Md) / info.Sd;
-        const float res = fmaxf(prob - q, 0.f);
-        any_res |= res > 0.f;
-        const float sr = res / Ee;
-        if (better(sr, idx, rv, ri)) {
-          rv = sr;
-          ri = idx;
+    }
+  };
+  auto reload = [&](int i) {
+    exact(i, load_logit<DT>(tbase, i), noise ? noise[i] : 1.f, dbase ? load_logit<DDT>(dbase, i) : 0.f);
+  };
+  // Upper bounds of entry i (of p / E and of the residual), a lower bound of its residual, whether its prob may
+  // be non-zero and whether its residual is surely positive. The lower bound of p / E is ubp * dn / up.
+  // log2(1 / sum) is folded into the exponent (one fma): sum <= vocab < 2^31, so it adds at most 31 * 2^-23
+  // (v_log_f32, 1 ulp) and 2^-24 (|x - shift| + 31) (the fma), which eps covers.
+  const float lsa = -__builtin_log2f(info.Sa), lsd = resid ? -__builtin_log2f(info.Sd) : 0.f;
+  struct Bounds {
+    float ubp, ubr, lbr;
+    bool live, sure;
+  };
+  auto bounds = [&](int i, float l, float E, float ld) {
+#pragma clang fp contract(off)
+    Bounds b;
+    const float rE = __builtin_amdgcn_rcpf(noise ? fmaxf(E, 1e-10f) : 1.f);
+    const float dp = (div ? l * z : l) - info.Ma;
+    const float pa = i == zap ? 0.f : exp2_fast(fmaf(dp, kL2E, lsa));
+    b.live = dp > kUnderflow;
+    b.ubp = pa * rE * up;
+    b.ubr = b.lbr = 0.f;
+    b.sure = false;
+    if (resid) {
+      const float qa = exp2_fast(fmaf((div ? ld * z : ld) - info.Md, kL2E, lsd));
+      const float slack = 2.f * eps * (pa + qa);
+      b.ubr = (fmaxf(pa - qa, 0.f) + slack) * rE * up;
+      b.lbr = fmaxf(pa - qa - slack, 0.f) * rE * dn;
+      b.sure = pa - qa - slack > 0.f;
+    }
+    return b;
+  };
+  // Pass over the span, in rounds of 8 entries a lane (v .. v+3 and v+kStep .. v+kStep+3).
+  constexpr int kStep = 4 * kThreads;
+  const int rounds = (v1 - v0 + 2 * kStep - 1) / (2 * kStep);
+  auto sweep = [&](auto&& visit) {
+    for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int v = v0 + r * 2 * kStep + u * kStep + 4 * threadIdx.x;
+        if (kVec && v + 4 <= v1) {
+          const float4 t4 = load_logit4<DT>(tbase, v);
+          const float4 e4 = noise ? *(const float4*)(noise + v) : make_float4(1.f, 1.f, 1.f, 1.f);
+          const float4 d4 = dbase ? load_logit4<DDT>(dbase, v) : make_float4(0.f, 0.f, 0.f, 0.f);
+          visit(v, t4.x, e4.x, d4.x);
+          visit(v + 1, t4.y, e4.y, d4.y);
+          visit(v + 2, t4.z, e4.z, d4.z);
+          visit(v + 3, t4.w, e4.w, d4.w);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (v + e < v1)
+              visit(v + e, load_logit<DT>(tbase, v + e), noise ? noise[v + e] : 1.f,
+                    dbase ? load_logit<DDT>(dbase, v + e) : 0.f);
         }
       }
     }
   };
-  // Same per-thread visiting order as row_stats; the aligned main loop has the loads of two steps (target,
-  // noise and draft rows) in flight before using them.
-  constexpr int kStep = 4 * kThreads;
-  int v = v0 + 4 * threadIdx.x;
-  if (kVec) {
-    for (; v + kStep + 4 <= v1; v += 2 * kStep) {
-      float4 t4[2], e4[2], d4[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        t4[u] = load_logit4<DT>(tbase, v + u * kStep);
-        e4[u] = noise ? *(const float4*)(noise + v + u * kStep) : make_float4(1.f, 1.f, 1.f, 1.f);
-        d4[u] = dbase ? load_logit4<DDT>(dbase, v + u * kStep) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const float l[4] = {t4[u].x, t4[u].y, t4[u].z, t4[u].w};
-        const float E[4] = {e4[u].x, e4[u].y, e4[u].z, e4[u].w};
-        const float ld[4] = {d4[u].x, d4[u].y, d4[u].z, d4[u].w};
-        body(v + u * kStep, l, E, ld);
-      }
-    }
-  }
-  for (; v < v1; v += kStep) {
-    float l[4], E[4] = {1.f, 1.f, 1.f, 1.f}, ld[4] = {0.f, 0.f, 0.f, 0.f};
-    if (kVec && v + 4 <= v1) {
-      const float4 t4 = load_logit4<DT>(tbase, v);
-      l[0] = t4.x, l[1] = t4.y, l[2] = t4.z, l[3] = t4.w;
-      if (noise) {
-        const float4 e4 = *(const float4*)(noise + v);
-        E[0] = e4.x, E[1] = e4.y, E[2] = e4.z, E[3] = e4.w;
-      }
-      if (dbase) {
-        const float4 d4 = load_logit4<DDT>(dbase, v);
-        ld[0] = d4.x, ld[1] = d4.y, ld[2] = d4.z, ld[3] = d4.w;
-      }
+  // Per lane: the entry with the largest upper bound (with its values) and the second-largest upper bound.
+  float b1p = -INFINITY, b2p = -INFINITY, b1r = -INFINITY, b2r = -INFINITY, lr = -INFINITY;
+  int i1p = -1, i1r = -1;
+  float cp[3] = {0.f, 0.f, 0.f}, cr[3] = {0.f, 0.f, 0.f};
+  bool sure = false, odd = false;
+  sweep([&](int i, float l, float E, float ld) {
+    const Bounds b = bounds(i, l, E, ld);
+    odd = odd || b.ubp != b.ubp || b.ubr != b.ubr;
+    if (b.ubp > b1p) {
+      b2p = b1p;
+      b1p = b.ubp;
+      i1p = i;
+      cp[0] = l, cp[1] = E, cp[2] = ld;
     } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool in = v + e < v1;
-        l[e] = in ? load_logit<DT>(tbase, v + e) : 0.f;
-        if (noise) E[e] = in ? noise[v + e] : 1.f;
-        if (dbase) ld[e] = in ? load_logit<DDT>(dbase, v + e) : 0.f;
-      }
+      b2p = fmaxf(b2p, b.ubp);
     }
-    body(v, l, E, ld);
+    if (resid) {
+      if (b.ubr > b1r) {
+        b2r = b1r;
+        b1r = b.ubr;
+        i1r = i;
+        cr[0] = l, cr[1] = E, cr[2] = ld;
+      } else {
+        b2r = fmaxf(b2r, b.ubr);
+      }
+      lr = fmaxf(lr, b.lbr);
+      sure = sure || b.sure;
+    }
+  });
+  // The largest lower bound of p / E in the span: the largest upper bound scaled down, less one rounding.
+  const float Lp = block_max(b1p, shf) * (dn / up) * (1.f - 2.384185791015625e-07f);
+  const float Lr = resid ? block_max(lr, shf + 4) : 0.f;
+  const bool sure_any = resid && __syncthreads_or(sure);
+  const bool tiny_p = !(Lp >= kTinyBest), tiny_r = resid && !(Lr >= kTinyBest);
+  if (sure) any_res = 1;
+  const bool rescan = odd || tiny_p || tiny_r || (resid && !sure_any) || b2p >= Lp || (resid && b2r >= Lr);
+  if (!rescan) {
+    const bool ep = i1p >= 0 && b1p >= Lp;
+    if (ep) exact(i1p, cp[0], cp[1], cp[2]);
+    if (resid && i1r >= 0 && b1r >= Lr && !(ep && i1r == i1p)) exact(i1r, cr[0], cr[1], cr[2]);
+  } else {
+    sweep([&](int i, float l, float E, float ld) {
+      const Bounds b = bounds(i, l, E, ld);
+      bool need = tiny_p ? b.live : !(b.ubp < Lp);
+      if (resid) need = need || (tiny_r ? b.live : !(b.ubr < Lr)) || (!sure_any && b.live);
+      if (need) reload(i);
+    });
   }
   block_argmax(pv, pi, shf, shi);
   Cand c{};
   c.p_val = pv;
   c.p_idx = pi;
-  if (info.resid_mode == 2) {
+  if (resid) {
     block_argmax(rv, ri, shf, shi);
     any_res = __syncthreads_or(any_res);
   }
@@ -593,8 +756,6 @@ int launch_all(const VParams& p, hipStream_t s, bool draft) {
   const int rows = p.S * (p.K + 1) + (draft ? p.S * p.K : 0);
   hipLaunchKernelGGL((row_stats<DT, DDT, kVec, true>), dim3(rows, p.nchunk), dim3(kThreads), 0, s, p);
   if ((rc = check_launch("row_stats"))) return rc;
-  hipLaunchKernelGGL((verify_decide<DT, DDT, true>), dim3(p.S), dim3(64), 0, s, p);
-  if ((rc = check_launch("verify_decide"))) return rc;
   hipLaunchKernelGGL((verify_resample<DT, DDT, kVec>), dim3(p.S, p.rchunk), dim3(kThreads), 0, s, p);
   if ((rc = check_launch("verify_resample"))) return rc;
   hipLaunchKernelGGL(verify_finish, dim3(p.S), dim3(kThreads), 0, s, p);

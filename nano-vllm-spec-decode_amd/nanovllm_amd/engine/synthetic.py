@@ -1,7 +1,8 @@
-"""Synthetic mixed prefill+decode steps: the request mix of a 2048-token-budget step at Qwen3-8B shapes (decode
-requests checking k guesses, then prefill chunks after a cached prefix), as the scheduler's schedule_mixed
-would hand it to the model runner (nanovllm/engine/scheduler.py, nanovllm/engine/model_runner.py:487-535).
-Used by the benchmark and the tests to build the same steps.
+"""Synthetic workloads of the attention hot path, shared by the benchmark and the tests: seeded paged KV caches
+with randomly permuted block tables (block size 256, as the reference's), queries, and the request mix of a
+2048-token-budget mixed step at Qwen3-8B shapes (decode requests checking k guesses, then prefill chunks
+after a cached prefix), as the scheduler's schedule_mixed would hand it to the model runner
+(nanovllm/engine/model_runner.py:487-535).
 """
 from __future__ import annotations
 
@@ -9,6 +10,33 @@ import math
 from types import SimpleNamespace
 
 import numpy as np
+import torch
+
+BLOCK = 256
+
+
+def paged_cache(device, ctx, Hkv, D, W=None, bs=BLOCK, extra_blocks=4, seed=0, tail=-1):
+    """Caches [NB, bs, Hkv, D] ~ N(0,1) bf16 and an int32 block table [B, W] whose used entries are a random
+    permutation of the free blocks; entries past ceil(ctx/bs) hold `tail` (-1, or a stale id)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    nblk = [max(1, math.ceil(c / bs)) for c in ctx]
+    NB = sum(nblk) + extra_blocks
+    W = W or max(nblk)
+    perm = torch.randperm(NB, device=device, generator=g).to(torch.int32)
+    tables = torch.full((len(ctx), W), tail, dtype=torch.int32, device=device)
+    at = 0
+    for b, nb in enumerate(nblk):
+        tables[b, :nb] = perm[at:at + nb]
+        at += nb
+    kc = torch.randn(NB, bs, Hkv, D, device=device, generator=g).to(torch.bfloat16)
+    vc = torch.randn(NB, bs, Hkv, D, device=device, generator=g).to(torch.bfloat16)
+    return kc, vc, tables
+
+
+def queries(device, tokens, Hq, D, seed=1):
+    """[tokens, Hq, D] ~ N(0,1) bf16."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    return torch.randn(tokens, Hq, D, device=device, generator=g).to(torch.bfloat16)
 
 
 def mixed_step_lengths(seed: int, num_decode: int = 48, k: int = 4, num_chunks: int = 3, budget: int = 2048):
