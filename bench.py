@@ -351,12 +351,30 @@ def bench_lm_head_verify(dev, S=64, K=4, V=151936, H=4096):
     w_bytes = V * H * 2
     logit_bytes = S * (K + 1) * V * 2
     verify_rate = logit_bytes / t_verify
+    # the fused path: sd_lm_head_verify, greedy (the GEMM's epilogue takes the argmax; no logits written)
+    from nanovllm_amd import _lib
+    lib = _lib.load()
+    acc = torch.empty(S, dtype=torch.int64, device=dev)
+    nxt = torch.empty(S, dtype=torch.int64, device=dev)
+    ws = torch.empty(lib.sd_lm_head_verify_workspace_size(S, K, V, H, 0), dtype=torch.uint8, device=dev)
+    from nanovllm_amd.layers.lm_head import pack_weight
+    wp = pack_weight(w)
+
+    def fused():
+        _lib.check(lib.sd_lm_head_verify(h.data_ptr(), H, S * (K + 1), None, wp.data_ptr(), V, H, drafts.data_ptr(),
+                                         nd.data_ptr(), None, None, 0, 0, None, None, S, K, None, 0, acc.data_ptr(),
+                                         nxt.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         torch.cuda.current_stream().cuda_stream), "sd_lm_head_verify")
+    t_fused = graph_timed(fused, reps=5)
     return dict(
         shape=f"[{S * (K + 1)}, {H}] x [{H}, {V}] bf16",
-        gemm_us=t_gemm * 1e6, gemm_tflops=flops / t_gemm / 1e12, gemm_mfma_frac=flops / t_gemm / 2.5e15,
-        gemm_weight_TBs=w_bytes / t_gemm / 1e12, verify_us=t_verify * 1e6, gemm_then_verify_us=t_both * 1e6,
-        fusion_saving_bound_us=2 * logit_bytes / verify_rate * 1e6,
-        timing="graph replays; logits bf16 as the engine's LM head writes them")
+        gemm_us=round(t_gemm * 1e6, 2), gemm_tflops=round(flops / t_gemm / 1e12, 1),
+        gemm_mfma_frac=round(flops / t_gemm / 2.5e15, 4), gemm_weight_TBs=round(w_bytes / t_gemm / 1e12, 3),
+        verify_us=round(t_verify * 1e6, 2), gemm_then_verify_us=round(t_both * 1e6, 2),
+        fused_us=round(t_fused * 1e6, 2), fused_tflops=round(flops / t_fused / 1e12, 1),
+        fused_mfma_frac=round(flops / t_fused / 2.5e15, 4), fused_weight_TBs=round(w_bytes / t_fused / 1e12, 3),
+        timing="graph replays; logits bf16 as the engine's LM head writes them; fused = sd_lm_head_verify "
+               "(hand-written MFMA GEMM with the argmax in its epilogue, T = 0, no logits written)")
 
 
 def bench_mixed_attention(dev, steps, warmup, layers=36):

@@ -193,6 +193,33 @@ int sd_verify_drafts(const void* logits, int32_t logits_dtype, int64_t logits_ro
                      size_t workspace_bytes, void* stream);
 
 /*
+ * LM head + verifier in one call. Replaces logits = compute_logits(hidden_states) (ParallelLMHead.forward,
+ * nanovllm/layers/embed_head.py:56-68: the logits_indices gather and F.linear) followed by verify_drafts
+ * (nanovllm/layers/sampler.py:28-103), as ModelRunner.run_verify calls them (nanovllm/engine/model_runner.py:
+ * 482-483). hidden: bf16 [hidden_rows, hidden_dim] rows with row stride hidden_row_stride (16-byte aligned rows);
+ * token row m = s*(K+1)+j of the verifier reads hidden row logits_indices[m] (clamped to the table), or row m
+ * when logits_indices is NULL. packed_weight: the LM head weight (bf16 [vocab, hidden_dim], rows contiguous) in
+ * the tile layout sd_lm_head_pack_weight writes, once per model (sd_lm_head_packed_weight_size bytes);
+ * hidden_dim a multiple of 32. logits[m, n] = bf16(fp32 sum over hidden_dim) as the library GEMM rounds them.
+ * With temperatures == NULL (every row greedy) the logits are never written unless logits_out is given: the
+ * GEMM's epilogue takes each row's first argmax. With temperatures, logits_out ([S*(K+1), vocab] bf16, row
+ * stride >= vocab) is required and the sampled rows are decided by sd_verify_drafts's passes over it. The
+ * other arguments and the outputs are sd_verify_drafts's. No counterpart in the reference for the packing (the
+ * reference's F.linear reads the weight as stored).
+ */
+size_t sd_lm_head_packed_weight_size(int32_t vocab, int32_t hidden_dim);
+int sd_lm_head_pack_weight(const void* weight, int32_t vocab, int32_t hidden_dim, void* packed_weight, void* stream);
+size_t sd_lm_head_verify_workspace_size(int32_t num_seqs, int32_t num_draft_slots, int32_t vocab, int32_t hidden_dim,
+                                        int32_t has_draft_logits);
+int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, int32_t hidden_rows,
+                      const int64_t* logits_indices, const void* packed_weight, int32_t vocab, int32_t hidden_dim,
+                      const int64_t* draft_token_ids, const int64_t* num_drafts, const float* temperatures,
+                      const void* draft_logits, int32_t draft_dtype, int64_t draft_row_stride, const float* uniforms,
+                      const float* exp_noise, int32_t num_seqs, int32_t num_draft_slots, void* logits_out,
+                      int64_t logits_out_row_stride, int64_t* num_accepted, int64_t* next_token, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
  * sd_verify_drafts without a workspace argument, for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference.
  * Same arguments, rule and results as sd_verify_drafts; the per-row statistics go to a scratch array of

@@ -26,6 +26,7 @@
 #include <atomic>
 #include <mutex>
 
+#include "lm_head.h"
 #include "sd_common.h"
 #include "../../include/sd_attn.h"
 
@@ -61,13 +62,6 @@ struct Cand {                     // per (seq, chunk)
   int32_t any_res;
   int32_t pad[3];
 };
-
-// true if (v, i) should replace (bv, bi) under torch.argmax order: NaN largest, then value, then lower index.
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-  const bool vn = v != v, bn = bv != bv;
-  if (vn || bn) return vn && (!bn || i < bi);
-  return v > bv || (v == bv && i < bi);
-}
 
 template <int DT>
 __device__ __forceinline__ float load_logit(const void* base, int64_t idx) {
@@ -562,7 +556,6 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
   const float* noise = p.noise ? p.noise + (int64_t)seq * p.V : nullptr;  // missing noise: E = 1
   const int zap = info.resid_mode == 1 && info.rejected ? info.guess : -1;  // n-gram: prob of the guess is 0
   const float kL2E = 1.4426950408889634f;
-  const float invSa = 1.f / info.Sa, invSd = resid ? 1.f / info.Sd : 0.f;
   const float eps = (fmaxf(fabsf(info.Ma), resid ? fabsf(info.Md) : 0.f) + 323.f) * 2.384185791015625e-07f;
   const float up = 1.f + 2.f * eps, dn = 1.f - 2.f * eps;
   const int v0 = chunk * p.rspan;
@@ -827,6 +820,68 @@ int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_
   return launch_all<SD_DTYPE_BF16, SD_DTYPE_BF16, false>(p, s, draft);
 }
 
+// ---- LM head + verifier ----
+
+// The first argmax of each token row over the LM head's per-workgroup results, into the span statistics of
+// a one-span row (decide_seq reads them); one wave per row, any tree order (the argmax order is total).
+__global__ __launch_bounds__(64) void lm_head_merge(const lmhead::TileBest* best, int tiles, RowStat* stats) {
+  const int m = blockIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int t = threadIdx.x; t < tiles; t += 64) {
+    const lmhead::TileBest b = best[(int64_t)m * tiles + t];
+    if (better(b.val, b.idx, bv, bi)) {
+      bv = b.val;
+      bi = b.idx;
+    }
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off);
+    const int oi = __shfl_xor(bi, off);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (threadIdx.x == 0) stats[m] = RowStat{-INFINITY, 0.f, bv, bi};
+}
+
+int lm_head_mb(int M) { return std::min(lmhead::kMaxMB, std::max(1, ((M + 31) / 32 + 1) / 2)); }
+
+// Token rows of the packed hidden operand: the GEMM grid's rows of workgroups times their rows.
+int64_t lm_head_mpad(int64_t M) {
+  const int MB = lm_head_mb((int)std::min<int64_t>(M, 0x7fffffff));
+  return (M + 64 * MB - 1) / (64 * MB) * (64 * MB);
+}
+
+struct LmLayout {
+  size_t best, stats, info, hp, total;
+};
+LmLayout lm_layout(int S, int K, int V, int H) {
+  const int64_t M = (int64_t)S * (K + 1);
+  const int tiles = (V + lmhead::kN - 1) / lmhead::kN;
+  LmLayout L;
+  L.best = 0;
+  L.stats = align256((size_t)M * tiles * sizeof(lmhead::TileBest));
+  L.info = align256(L.stats + (size_t)M * sizeof(RowStat));
+  L.hp = align256(L.info + (size_t)S * sizeof(SeqInfo));
+  L.total = align256(L.hp + (size_t)lm_head_mpad(M) * H * 2);
+  return L;
+}
+
+int launch_lm_head(const lmhead::Args& a, hipStream_t s) {
+  const int MB = lm_head_mb(a.M);
+  const dim3 grid((unsigned)a.tiles, (unsigned)(a.Mpad / (64 * MB)));
+  switch (MB) {
+    case 1: hipLaunchKernelGGL(lmhead::lm_head_gemm<1>, grid, dim3(lmhead::kThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(lmhead::lm_head_gemm<2>, grid, dim3(lmhead::kThreads), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(lmhead::lm_head_gemm<3>, grid, dim3(lmhead::kThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(lmhead::lm_head_gemm<4>, grid, dim3(lmhead::kThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL(lmhead::lm_head_gemm<5>, grid, dim3(lmhead::kThreads), 0, s, a); break;
+  }
+  return check_launch("lm_head_gemm");
+}
+
 // Scratch of the allocation-free entry point: one copy per GPU (a __device__ variable lives in every device's
 // code object), held until the process ends. Its host-side name is not a device address: kernels get the
 // address hipGetSymbolAddress returns on the current device, looked up once per device.
@@ -916,4 +971,109 @@ extern "C" int sd_verify_drafts_noalloc(const void* logits, int32_t logits_dtype
   return run_verify(who, logits, logits_dtype, logits_row_stride, draft_token_ids, num_drafts, temperatures,
                     draft_logits, draft_dtype, draft_row_stride, uniforms, exp_noise, num_seqs, num_draft_slots, vocab,
                     num_accepted, next_token, ws, kStaticScratchBytes, stream);
+}
+
+extern "C" size_t sd_lm_head_packed_weight_size(int32_t vocab, int32_t hidden_dim) {
+  if (vocab <= 0 || hidden_dim <= 0 || hidden_dim % lmhead::kK) return 0;
+  return (size_t)((vocab + lmhead::kN - 1) / lmhead::kN) * lmhead::kN * hidden_dim * 2;
+}
+
+extern "C" int sd_lm_head_pack_weight(const void* weight, int32_t vocab, int32_t hidden_dim, void* packed,
+                                     void* stream) {
+  const char* who = "sd_lm_head_pack_weight";
+  if (vocab <= 0 || hidden_dim <= 0) return fail(kBadArgument, "%s: bad sizes (vocab %d, hidden %d)", who, vocab,
+                                                 hidden_dim);
+  if (hidden_dim % lmhead::kK)
+    return fail(kUnsupported, "%s: hidden size %d is not a multiple of %d", who, hidden_dim, lmhead::kK);
+  if (!weight || !packed) return fail(kBadArgument, "%s: null pointer", who);
+  if (((uintptr_t)weight | (uintptr_t)packed) % 16) return fail(kUnsupported, "%s: 16-byte aligned buffers", who);
+  const int tiles = (vocab + lmhead::kN - 1) / lmhead::kN;
+  const int64_t chunks = (int64_t)tiles * (hidden_dim / 32) * lmhead::kN * 4;
+  hipLaunchKernelGGL(lmhead::lm_head_pack_weight, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)weight, vocab, hidden_dim, tiles, (uint16_t*)packed);
+  return check_launch(who);
+}
+
+extern "C" size_t sd_lm_head_verify_workspace_size(int32_t num_seqs, int32_t num_draft_slots, int32_t vocab,
+                                                   int32_t hidden_dim, int32_t has_draft_logits) {
+  if (num_seqs <= 0 || num_draft_slots < 0 || vocab <= 0 || hidden_dim <= 0) return 0;
+  return std::max(lm_layout(num_seqs, num_draft_slots, vocab, hidden_dim).total,
+                  verify_layout(num_seqs, num_draft_slots, vocab, has_draft_logits && num_draft_slots > 0).total);
+}
+
+extern "C" int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, int32_t hidden_rows,
+                                 const int64_t* logits_indices, const void* packed_weight, int32_t vocab,
+                                 int32_t hidden_dim, const int64_t* draft_token_ids, const int64_t* num_drafts,
+                                 const float* temperatures, const void* draft_logits, int32_t draft_dtype,
+                                 int64_t draft_row_stride, const float* uniforms, const float* exp_noise, int32_t num_seqs,
+                                 int32_t num_draft_slots, void* logits_out, int64_t logits_out_row_stride,
+                                 int64_t* num_accepted, int64_t* next_token, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  const char* who = "sd_lm_head_verify";
+  const int S = num_seqs, K = num_draft_slots, V = vocab, H = hidden_dim;
+  if (S < 0 || K < 0 || K > 63 || V <= 0 || H <= 0)
+    return fail(kBadArgument, "%s: bad sizes (seqs %d, draft slots %d (max 63), vocab %d, hidden %d)", who, S, K, V, H);
+  if (S == 0) return kOk;
+  if (H % lmhead::kK)
+    return fail(kUnsupported, "%s: hidden size %d is not a multiple of %d", who, H, lmhead::kK);
+  if (!hidden || !packed_weight || !num_accepted || !next_token || (K > 0 && (!draft_token_ids || !num_drafts)))
+    return fail(kBadArgument, "%s: null pointer", who);
+  if (hidden_row_stride < H || ((uintptr_t)hidden | (uintptr_t)packed_weight) % 16 || hidden_row_stride % 8)
+    return fail(kUnsupported, "%s: hidden and weight must be 16-byte aligned rows (row stride a multiple of 8)", who);
+  if (temperatures && !logits_out)
+    return fail(kBadArgument, "%s: sampled rows read the logits again: logits_out is required with temperatures",
+                who);
+  if (logits_out && (logits_out_row_stride < V || (uintptr_t)logits_out % 2))
+    return fail(kBadArgument, "%s: logits_out needs a row stride >= vocab", who);
+  const int64_t M = (int64_t)S * (K + 1);
+  if (M > 0x7fffffff / 64) return fail(kUnsupported, "%s: too many rows", who);
+  if (hidden_rows < (logits_indices ? 1 : M))
+    return fail(kBadArgument, "%s: hidden has %d rows (needs %s)", who, hidden_rows,
+                logits_indices ? "at least 1" : "one per token row");
+  const size_t need = sd_lm_head_verify_workspace_size(S, K, V, H, draft_logits != nullptr);
+  if (!workspace || workspace_bytes < need)
+    return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, need);
+  const LmLayout lay = lm_layout(S, K, V, H);
+  hipStream_t s = (hipStream_t)stream;
+  lmhead::Args a{};
+  a.Mpad = (int32_t)lm_head_mpad(M);
+  a.hp = (const uint16_t*)((uint8_t*)workspace + lay.hp);
+  a.M = (int32_t)M;
+  a.wp = (const uint16_t*)packed_weight;
+  a.V = V;
+  a.H = H;
+  a.logits = (uint16_t*)logits_out;
+  a.logits_stride = logits_out_row_stride;
+  a.logits_vec = (uintptr_t)logits_out % 8 == 0 && logits_out_row_stride % 4 == 0;
+  a.best = (lmhead::TileBest*)((uint8_t*)workspace + lay.best);
+  a.tiles = (V + lmhead::kN - 1) / lmhead::kN;
+  const int64_t hchunks = (int64_t)(H / 32) * a.Mpad * 4;
+  hipLaunchKernelGGL(lmhead::lm_head_pack_hidden, dim3((unsigned)((hchunks + 255) / 256)), dim3(256), 0, s,
+                     (const uint16_t*)hidden, hidden_row_stride, hidden_rows, logits_indices, a.M, a.Mpad, H,
+                     (uint16_t*)a.hp);
+  int rc = check_launch("lm_head_pack_hidden");
+  if (rc) return rc;
+  if ((rc = launch_lm_head(a, s))) return rc;
+  if (temperatures)  // sampled rows: the verifier's own passes over the stored logits
+    return run_verify(who, logits_out, SD_DTYPE_BF16, logits_out_row_stride, draft_token_ids, num_drafts, temperatures,
+                      draft_logits, draft_dtype, draft_row_stride, uniforms, exp_noise, S, K, V, num_accepted,
+                      next_token, workspace, workspace_bytes, stream);
+  VParams p{};
+  p.logits = logits_out;  // read only for sampled rows (none here)
+  p.logits_stride = logits_out_row_stride;
+  p.drafts = draft_token_ids;
+  p.num_drafts = num_drafts;
+  p.S = S;
+  p.K = K;
+  p.V = V;
+  p.nchunk = 1;
+  p.span = V;
+  p.out_a = num_accepted;
+  p.out_next = next_token;
+  p.stats = (RowStat*)((uint8_t*)workspace + lay.stats);
+  p.info = (SeqInfo*)((uint8_t*)workspace + lay.info);
+  hipLaunchKernelGGL(lm_head_merge, dim3((unsigned)M), dim3(64), 0, s, a.best, a.tiles, p.stats);
+  if ((rc = check_launch("lm_head_merge"))) return rc;
+  hipLaunchKernelGGL((verify_decide<SD_DTYPE_BF16, SD_DTYPE_BF16, false>), dim3(S), dim3(64), 0, s, p);
+  return check_launch("verify_decide");
 }

@@ -45,6 +45,12 @@ SIGNATURES = {
     "sd_verify_drafts": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64,
                                 _c_void_p, _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p, _c_void_p, _size,
                                 _c_void_p]),
+    "sd_lm_head_packed_weight_size": (_size, [_i32, _i32]),
+    "sd_lm_head_pack_weight": (_i32, [_c_void_p, _i32, _i32, _c_void_p, _c_void_p]),
+    "sd_lm_head_verify_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32]),
+    "sd_lm_head_verify": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _c_void_p,
+                                 _c_void_p, _c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _i64,
+                                 _c_void_p, _c_void_p, _c_void_p, _size, _c_void_p]),
     "sd_verify_drafts_noalloc": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32,
                                         _i64, _c_void_p, _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p,
                                         _c_void_p]),
