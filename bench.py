@@ -695,7 +695,8 @@ def main():
     ap.add_argument("--skip-extras", action="store_true", help="headline only (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="leave out the CPU baseline (for profiling)")
     ap.add_argument("--only", choices=["qk_norm_rope_store", "draft_step_inputs", "kv_store", "lm_head_verify",
-                                       "verify_sampler", "mixed_step_full", "mixed_step_attention", "prefill_kernel"],
+                                       "verify_sampler", "mixed_step_full", "mixed_step_attention", "prefill_kernel",
+                                       "verify_attention_sweep"],
                     help="run one secondary workload alone and print its JSON (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
@@ -720,7 +721,8 @@ def main():
               "verify_sampler": lambda: bench_sampler(dev, args.steps, args.warmup),
               "mixed_step_full": lambda: bench_mixed_step_full(dev),
               "mixed_step_attention": lambda: bench_mixed_attention(dev, max(5, args.steps // 10), 2),
-              "prefill_kernel": lambda: bench_prefill(dev)}[args.only]
+              "prefill_kernel": lambda: bench_prefill(dev),
+              "verify_attention_sweep": lambda: bench_verify_sweep(dev)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
     head = bench_verify_attention(dev, args.steps, args.warmup)

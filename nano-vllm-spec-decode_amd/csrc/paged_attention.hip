@@ -21,6 +21,7 @@
 //   S^T[16 keys x 16 rows] = K[16 x 128] . Q^T      A = K straight from HBM into registers (16 B per
 //                                                    lane, 64 contiguous bytes per key row per load),
 //                                                    B = Q in registers for the whole item
+//                                                    (three or four row tiles: read from LDS)
 //   O^T[16 d x 16 rows]   += V^T[16 x 32] . P^T      A = V^T read transposed from LDS with
 //                                                    ds_read_b64_tr_b16, B = P straight from S^T's
 //                                                    accumulators (the key order inside the 32-key
@@ -50,7 +51,7 @@ constexpr int kObRow = kD + 4;                 // fp32 row stride of the merge b
 constexpr int kMaxRows = 64;                   // 16-row tiles: at most 4
 constexpr int kMaxBlocks = 1024;               // block-table entries staged in LDS per item
 constexpr int kMlBytes = kResidues * kMaxRows * 2 * 4;
-constexpr int kMergeRows = 32;                 // rows merged in LDS (row tiles 1-2)
+constexpr int kMergeRows = 32;                 // rows merged in LDS per pass (two row tiles)
 constexpr int kObBytes = kResidues * kMergeRows * kObRow * 4;
 
 // LDS of a workgroup with `waves` waves: one V buffer per wave (when the workgroup merges all eight
@@ -61,6 +62,16 @@ constexpr int stage_bytes(int waves) {
 }
 constexpr int ml_bytes(int waves) { return waves == kResidues ? kMlBytes : 0; }
 constexpr int lds_bytes(int waves) { return stage_bytes(waves) + ml_bytes(waves) + kMaxBlocks * 4; }
+// Three and four row tiles read Q from LDS at every tile instead of holding it in registers (16 registers per
+// row tile), so that three fit in 256 registers and run two waves per SIMD. Q rows of 256 B, the 16-byte
+// chunk c of row r at c ^ (r % 16): the 16 lanes of a read take 16 different chunks. With eight waves the Q
+// rows sit in the stage bytes past the V buffers, which only the merge uses; otherwise past the block ids.
+constexpr int q_lds_bytes(int rt) { return rt >= 3 ? rt * 16 * kD * 2 : 0; }
+constexpr int q_lds_offset(int waves) { return waves == kResidues ? waves * kVBuf : lds_bytes(waves); }
+constexpr int lds_bytes_rt(int waves, int rt) {
+  return waves == kResidues ? lds_bytes(waves) : lds_bytes(waves) + q_lds_bytes(rt);
+}
+static_assert(kResidues * kVBuf + q_lds_bytes(4) <= stage_bytes(kResidues), "Q rows fit past the V buffers");
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
@@ -178,12 +189,13 @@ __device__ __forceinline__ float merge_scale(float m_r, float M) {
 }
 
 // One (item, KV head h) with the workgroup's kWaves waves, owning residues bx*kWaves .. +kWaves-1; `lds`
-// holds lds_bytes(kWaves). (kCaller only separates the instantiations made from different kernels: the
+// holds lds_bytes_rt(kWaves, RT). (kCaller only separates the instantiations made from different kernels: the
 // host compilation pass rejects one instantiation reached from two kernels.)
 template <int RT, bool kVarlen, bool kPaged, int kWaves, int kCaller = 0, bool kNT = false>
 __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int item, int h, int bx) {
   constexpr bool kMergeHere = kWaves == kResidues;
   constexpr int kStageBytes = stage_bytes(kWaves);
+  constexpr bool kQLds = q_lds_bytes(RT) > 0;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -234,23 +246,51 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   // Per-row visible-key limit (bottom-right causal: query i sees Lk - Lq + i + 1 keys) and the Q operand
   // (B of S^T): lane holds row 16*rt + r16, d = 32*ks + 8*grp + e.
   int lim[RT];
-  bf16x8 qv[RT][4];
+  bf16x8 qv[kQLds ? 1 : RT][4];
+  uint8_t* qlds = lds + q_lds_offset(kWaves);
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int row = rt * 16 + r16;
     if (row < rows) {
       const int i = it.p0 + row / p.g;
-      const int hq = h * p.g + row % p.g;
       lim[rt] = min(max(it.Lk - it.Lq + i + 1, 0), kmax);
-      const uint16_t* qp = p.q + (int64_t)(it.q_start + i) * p.q_stride + hq * kD + 8 * grp;
+      if constexpr (!kQLds) {
+        const int hq = h * p.g + row % p.g;
+        const uint16_t* qp = p.q + (int64_t)(it.q_start + i) * p.q_stride + hq * kD + 8 * grp;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qv[rt][ks] = *(const bf16x8*)(qp + 32 * ks);
+        for (int ks = 0; ks < 4; ++ks) qv[rt][ks] = *(const bf16x8*)(qp + 32 * ks);
+      }
     } else {
       lim[rt] = kmax;  // padding row: Q = 0 keeps its scores finite; never written
+      if constexpr (!kQLds) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qv[rt][ks] = bf16x8{};
+        for (int ks = 0; ks < 4; ++ks) qv[rt][ks] = bf16x8{};
+      }
     }
   }
+  if constexpr (kQLds) {
+    // Q rows into LDS, one 16-byte chunk per thread and step (padding rows zero).
+    constexpr int kChunks = RT * 16 * 16;
+    for (int ci = tid; ci < kChunks; ci += kWaves * kWave) {
+      const int row = ci / 16, c = ci % 16;
+      u32x4 v = {0, 0, 0, 0};
+      if (row < rows) {
+        const int i = it.p0 + row / p.g;
+        const int hq = h * p.g + row % p.g;
+        v = *(const u32x4*)(p.q + (int64_t)(it.q_start + i) * p.q_stride + hq * kD + 8 * c);
+      }
+      *(u32x4*)(qlds + row * 256 + 16 * (c ^ (row % 16))) = v;
+    }
+    __syncthreads();
+  }
+  // Q operand of row tile rt, k-step ks (B of S^T): from registers, or the lane's chunk 4 ks + grp of row
+  // 16 rt + r16 in LDS.
+  auto q_frag = [&](int rt, int ks) -> bf16x8 {
+    if constexpr (kQLds)
+      return *(const bf16x8*)(qlds + (rt * 16 + r16) * 256 + 16 * ((4 * ks + grp) ^ r16));
+    else
+      return qv[rt][ks];
+  };
 
   float m[RT], l[RT];
   f32x4 o[8][RT];
@@ -265,11 +305,12 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   uint8_t* vbuf = lds + wave * kVBuf;
   // V^T reads (ds_read_b64_tr_b16): source lane reads 4 d of key tl (+16 for the second half) at
   // d = 16*dt + 4*(lane%4): chunk 2*dt + (lane%4)/2, byte 8*(lane%2) inside it.
+  // That chunk, (2 dt + (lane%4)/2) ^ 2 (tl%8), is 2 (dt ^ (tl%8)) + (lane%4)/2: one xor per read from two
+  // lane constants (no per-d-tile offset registers).
   const int tl = 4 * grp + r16 / 4;
-  uint32_t vt_off[8];
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-    vt_off[dt] = tl * 256 + 8 * (lane % 2) + 16 * (((2 * dt + (lane % 4) / 2) ^ (2 * (tl % 8))));
+  const uint32_t vt_base = tl * 256 + 8 * (lane % 2) + 16 * ((lane % 4) / 2);
+  const uint32_t vt_x = 32 * (tl % 8);
+  auto vt_off = [&](int dt) { return vt_base + (vt_x ^ (32u * dt)); };
 
   // Tile addressing: K / V base of tile jt (wave-uniform byte pointers; keys past the item's end read the
   // tile's first key instead: finite data, masked out in the softmax). An invalid block id (bad table)
@@ -334,9 +375,10 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   };
   // V^T operand of d-tile dt (16 d x 32 keys) from this wave's LDS buffer: two transposed reads.
   auto read_vt = [&](int dt) {
-    const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[dt]));
+    const uint32_t off = vt_off(dt);
+    const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(vbuf + off));
     const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) v4i16*)(vbuf + vt_off[dt] + 16 * 256));
+        (__attribute__((address_space(3))) v4i16*)(vbuf + off + 16 * 256));
     const short e8 __attribute__((ext_vector_type(8))) = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     return __builtin_bit_cast(bf16x8, e8);
   };
@@ -345,27 +387,38 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   // softmax and O^T += V^T P^T.
   auto compute = [&](int jt, bool tile_ok, bf16x8 (&kr)[2][4], bool has_next, const TileSrc& next) {
     const int t0 = jt * kTile;
-    f32x4 s[2][RT];
+    // S^T of row tile rt into s[.][rt] (or s[.][0] when the row tiles are interleaved).
+    constexpr bool kInterleave = kQLds;  // three or four row tiles: S^T of one row tile live at a time
+    f32x4 s[2][kInterleave ? 1 : RT];
+    auto scores = [&](int rt, int slot) {
+      s[0][slot] = s[1][slot] = f32x4{};
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        f32x4 acc = f32x4{};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc = mfma16(kr[kt][ks], qv[rt][ks], acc);
-        s[kt][rt] = acc;
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 qf = q_frag(rt, ks);
+        s[0][slot] = mfma16(kr[0][ks], qf, s[0][slot]);
+        s[1][slot] = mfma16(kr[1][ks], qf, s[1][slot]);
       }
-    if (has_next) load_k(next, kr);
+    };
+    if constexpr (!kInterleave) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) scores(rt, rt);
+      if (has_next) load_k(next, kr);
+    }
     bf16x8 pb[RT];
     const int tok0 = t0 + 4 * grp;  // keys of this lane: tok0 + (e%4) + 16*(e/4)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
+      const int slot = kInterleave ? 0 : rt;
+      if constexpr (kInterleave) {
+        scores(rt, 0);
+        if (rt == RT - 1 && has_next) load_k(next, kr);
+      }
       const int lim_e = (tile_ok ? lim[rt] : t0) - tok0;
       float x[8];
       float mx = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        x[e] = (e % 4) + 16 * (e / 4) < lim_e ? s[e / 4][rt][e % 4] * p.scale_log2 : -INFINITY;
+        x[e] = (e % 4) + 16 * (e / 4) < lim_e ? s[e / 4][slot][e % 4] * p.scale_log2 : -INFINITY;
         mx = fmaxf(mx, x[e]);
       }
       mx = quad_max(mx);
@@ -450,9 +503,9 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
     return;
   } else {
     // ---- merge the eight residues in order: every wave parks its O in LDS, then each thread finishes
-    // eight consecutive d of one row with the same fma chain as attn_combine ----
-    static_assert(RT * 16 <= kMergeRows, "in-workgroup merge holds at most 32 rows");
-    __syncthreads();  // all V^T reads done: the V buffers become the O store
+    // eight consecutive d of one row with the same fma chain as attn_combine; 32 rows per pass ----
+    static_assert(RT * 16 <= kMaxRows, "row tiles");
+    __syncthreads();  // all V^T (and Q) reads done: the stage bytes become the O store
     float* ml = (float*)(lds + kStageBytes);  // [residue][kMaxRows][2]
     float* ob = (float*)lds;                  // [residue][kMergeRows][kObRow]
     if (grp == 0) {
@@ -462,42 +515,50 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
         ml[(wave * kMaxRows + rt * 16 + r16) * 2 + 1] = l[rt];
       }
     }
+    constexpr int kPassTiles = kMergeRows / 16;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      if (rt * 16 + r16 >= rows) continue;  // padding rows are never read (LDS stores are the merge's cost)
-      float* orow = ob + (wave * kMergeRows + rt * 16 + r16) * kObRow + 4 * grp;
+    for (int pass = 0; pass * kPassTiles < RT; ++pass) {
+      if (pass > 0) __syncthreads();  // the previous pass's reads of the O store are done
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) *(f32x4*)(orow + 16 * dt) = o[dt][rt];
-    }
-    __syncthreads();
-    constexpr int kThreads = kWaves * kWave;
-    for (int e0 = tid * 8; e0 < RT * 16 * kD; e0 += kThreads * 8) {
-      const int row = e0 / kD, d0 = e0 % kD;
-      if (row >= rows) continue;
-      float M = -INFINITY;
+      for (int rt = pass * kPassTiles; rt < RT && rt < (pass + 1) * kPassTiles; ++rt) {
+        if (rt * 16 + r16 >= rows) continue;  // padding rows are never read (LDS stores are the merge's cost)
+        float* orow = ob + (wave * kMergeRows + (rt - pass * kPassTiles) * 16 + r16) * kObRow + 4 * grp;
 #pragma unroll
-      for (int r = 0; r < kResidues; ++r) M = fmaxf(M, ml[(r * kMaxRows + row) * 2]);
-      float L = 0.f;
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int r = 0; r < kResidues; ++r) {
-        const float f = merge_scale(ml[(r * kMaxRows + row) * 2], M);
-        L = __builtin_fmaf(ml[(r * kMaxRows + row) * 2 + 1], f, L);
-        const float* src = ob + (r * kMergeRows + row) * kObRow + d0;
-        const f32x4 a = *(const f32x4*)src, b = *(const f32x4*)(src + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[e] = __builtin_fmaf(a[e], f, acc[e]);
-          acc[4 + e] = __builtin_fmaf(b[e], f, acc[4 + e]);
-        }
+        for (int dt = 0; dt < 8; ++dt) *(f32x4*)(orow + 16 * dt) = o[dt][rt];
       }
-      const int i = it.p0 + row / p.g;
-      const int hq = h * p.g + row % p.g;
-      u32x4 w;
+      __syncthreads();
+      constexpr int kThreads = kWaves * kWave;
+      const int row0 = pass * kMergeRows;
+      const int pass_rows = min(RT * 16 - row0, kMergeRows);
+      for (int e0 = tid * 8; e0 < pass_rows * kD; e0 += kThreads * 8) {
+        const int prow = e0 / kD, d0 = e0 % kD;
+        const int row = row0 + prow;
+        if (row >= rows) continue;
+        float M = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = cvt_bf16x2(L == 0.f ? 0.f : acc[2 * e] / L, L == 0.f ? 0.f : acc[2 * e + 1] / L);
-      *(u32x4*)(p.out + (int64_t)(it.q_start + i) * p.out_stride + hq * kD + d0) = w;
+        for (int r = 0; r < kResidues; ++r) M = fmaxf(M, ml[(r * kMaxRows + row) * 2]);
+        float L = 0.f;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < kResidues; ++r) {
+          const float f = merge_scale(ml[(r * kMaxRows + row) * 2], M);
+          L = __builtin_fmaf(ml[(r * kMaxRows + row) * 2 + 1], f, L);
+          const float* src = ob + (r * kMergeRows + prow) * kObRow + d0;
+          const f32x4 a = *(const f32x4*)src, b = *(const f32x4*)(src + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            acc[e] = __builtin_fmaf(a[e], f, acc[e]);
+            acc[4 + e] = __builtin_fmaf(b[e], f, acc[4 + e]);
+          }
+        }
+        const int i = it.p0 + row / p.g;
+        const int hq = h * p.g + row % p.g;
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = cvt_bf16x2(L == 0.f ? 0.f : acc[2 * e] / L, L == 0.f ? 0.f : acc[2 * e + 1] / L);
+        *(u32x4*)(p.out + (int64_t)(it.q_start + i) * p.out_stride + hq * kD + d0) = w;
+      }
     }
   }
 }
@@ -515,7 +576,7 @@ __device__ __forceinline__ int rotated_head(const Params& p, int y, int z) {
 
 template <int RT, bool kVarlen, bool kPaged, int kWaves>
 __global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes(kWaves)];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes_rt(kWaves, RT)];
   const int h = rotated_head(p, blockIdx.y, blockIdx.z);
   if constexpr (kVarlen) {
     attn_body<RT, kVarlen, kPaged, kWaves>(p, lds, blockIdx.z, h, blockIdx.x);
@@ -1035,11 +1096,13 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan(const int32_t* __res
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// CUs of the current device (the number of 8-wave workgroups it runs at once), queried once per device.
-int wave_slots() {
+// CUs of the device that runs `stream` (the number of 8-wave workgroups it runs at once), queried once per
+// device. The null stream is the current device's.
+int wave_slots(hipStream_t stream) {
   static std::atomic<int> cached[64];  // per device; 0 until first queried (threads may race to fill it)
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  hipDevice_t dev = 0;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess && hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev < 0 || dev >= 64) return 256;
   int cus = cached[dev].load(std::memory_order_relaxed);
   if (!cus) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
@@ -1094,7 +1157,7 @@ static_assert(kVarlenRT == 2, "mixed_fwd runs the residue body with two row tile
 // residues per workgroup and more workgroups, with the merge in attn_combine.
 int residue_waves(int64_t items, int Hkv, int RT) {
   const int64_t pairs = items * Hkv;
-  if (RT <= 2 && pairs >= 256) return 8;
+  if (RT <= 3 && pairs >= 256) return 8;
   if (pairs >= 128) return 4;
   if (pairs >= 32) return 2;
   return 1;
@@ -1120,7 +1183,7 @@ void launch_rt(int waves, dim3 items_grid, hipStream_t s, const Params& p) {
   }
 }
 
-// Row tiles 3 and 4 need more than 256 registers per wave, so they never run eight waves per workgroup.
+// Four row tiles need more than 256 registers per wave, so they never run eight waves per workgroup.
 template <int RT, bool kVarlen, bool kPaged>
 void launch_rt_small(int waves, dim3 items_grid, hipStream_t s, const Params& p) {
   const dim3 grid(kResidues / waves, items_grid.y, items_grid.z);
@@ -1136,7 +1199,7 @@ void launch_fwd(int RT, int waves, dim3 grid, hipStream_t s, const Params& p) {
   switch (RT) {
     case 1: launch_rt<1, kVarlen, kPaged>(waves, grid, s, p); break;
     case 2: launch_rt<2, kVarlen, kPaged>(waves, grid, s, p); break;
-    case 3: launch_rt_small<3, kVarlen, kPaged>(waves, grid, s, p); break;
+    case 3: launch_rt<3, kVarlen, kPaged>(waves, grid, s, p); break;
     default: launch_rt_small<4, kVarlen, kPaged>(waves, grid, s, p); break;
   }
 }
@@ -1198,7 +1261,7 @@ int decode_run(const char* who, bool planned, const void* q, int64_t q_token_str
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, need);
 
   Params p{};
-  p.wave_slots = wave_slots();
+  p.wave_slots = wave_slots((hipStream_t)stream);
   p.q = (const uint16_t*)q;
   p.q_stride = q_token_stride;
   p.k = (const uint16_t*)k_cache;
@@ -1392,7 +1455,7 @@ int varlen_run(const char* who, bool planned, const void* q, int64_t q_token_str
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
 
   Params p{};
-  p.wave_slots = wave_slots();
+  p.wave_slots = wave_slots((hipStream_t)stream);
   p.q = (const uint16_t*)q;
   p.q_stride = q_token_stride;
   p.k = (const uint16_t*)k;

@@ -891,10 +891,15 @@ static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_mutex;
 
-int static_scratch(const char* who, void** out) {
+// The scratch of the device that runs `stream`, which must be the current device (hipGetSymbolAddress answers
+// for the current device only).
+int static_scratch(const char* who, hipStream_t stream, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return fail(kLaunchFailed, "%s: no current device (or device index >= %d)", who, kMaxDevices);
+  hipDevice_t sdev = dev;
+  if (hipStreamGetDevice(stream, &sdev) == hipSuccess && sdev != dev)
+    return fail(kBadArgument, "%s: the stream belongs to device %d, the current device is %d", who, (int)sdev, dev);
   void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
   if (!ptr) {
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
@@ -966,7 +971,7 @@ extern "C" int sd_verify_drafts_noalloc(const void* logits, int32_t logits_dtype
                 "point holds; use sd_verify_drafts with a workspace", who, num_seqs, num_draft_slots, need,
                 kStaticScratchBytes);
   void* ws = nullptr;
-  const int rc = static_scratch(who, &ws);
+  const int rc = static_scratch(who, (hipStream_t)stream, &ws);
   if (rc) return rc;
   return run_verify(who, logits, logits_dtype, logits_row_stride, draft_token_ids, num_drafts, temperatures,
                     draft_logits, draft_dtype, draft_row_stride, uniforms, exp_noise, num_seqs, num_draft_slots, vocab,

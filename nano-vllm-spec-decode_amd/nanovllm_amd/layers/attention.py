@@ -49,8 +49,9 @@ def _as_rows(x: torch.Tensor, heads: int, head_dim: int) -> torch.Tensor:
     return x
 
 
-# (owner, key) of the decode order held by the decode workspace (set by the last sd_paged_decode_plan call).
-_decode_plan_in_workspace = None
+# Per decode workspace (keyed by its address, so per device): (owner, key) of the decode order it holds, set
+# by the last sd_paged_decode_plan call into it.
+_decode_plans: dict = {}
 
 
 def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -62,7 +63,6 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     then dispatched longest first, in an order planned once per owner and batch shape and reused by later
     layers (the order never changes results). A plan made while a graph is captured is only reused within
     captures, one made eagerly only eagerly, so that every graph holds the plan it replays with."""
-    global _decode_plan_in_workspace
     B, n, Hq, hd = q.shape
     NB, bs, Hkv, _ = k_cache.shape
     _require(q.dtype == torch.bfloat16 and k_cache.dtype == torch.bfloat16, "paged_decode_attention: bf16 required")
@@ -81,14 +81,14 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     if plan_owner is not None and B > 0:
         capturing = torch.cuda.is_current_stream_capturing()
         key = (context_lens.data_ptr(), B, n, Hq, Hkv, ws.data_ptr(), ws.numel(), capturing)
-        cached = _decode_plan_in_workspace
+        cached = _decode_plans.get(ws.data_ptr())
         if not (cached is not None and cached[0] is plan_owner and cached[1] == key):
             _lib.check(lib.sd_paged_decode_plan(context_lens.data_ptr(), B, n, Hq, Hkv, ws.data_ptr(), ws.numel(),
                                                 stream), "sd_paged_decode_plan")
-            _decode_plan_in_workspace = (plan_owner, key)
+            _decode_plans[ws.data_ptr()] = (plan_owner, key)
         fn = lib.sd_paged_decode_planned
     else:
-        _decode_plan_in_workspace = None  # an unplanned call may write partials over the order
+        _decode_plans.pop(ws.data_ptr(), None)  # an unplanned call may write partials over the order
     rc = fn(qr.data_ptr(), qr.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), NB, bs, context_lens.data_ptr(),
             block_tables.data_ptr(), W, B, n, Hq, Hkv, hd, scale, out.data_ptr(), out.stride(0), ws.data_ptr(),
             ws.numel(), stream)
@@ -96,9 +96,10 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     return out
 
 
-# (owner, key) of the varlen plan held by the varlen workspace (set by the last sd_varlen_plan call). The
-# owner is held here (not tagged: the Context dataclass has slots), so its id cannot be reused meanwhile.
-_plan_in_workspace = None
+# Per varlen workspace (keyed by its address, so per device): (owner, key) of the plan it holds, set by the
+# last sd_varlen_plan call into it. The owner is held here (not tagged: the Context dataclass has slots), so
+# its id cannot be reused meanwhile.
+_varlen_plans: dict = {}
 plan_stats = {"plans": 0, "reuses": 0}
 
 
@@ -113,7 +114,6 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     The work lists derived from them are then computed once and reused by every later call with the same
     owner and sizes, as long as no other plan has replaced them in the varlen workspace. Never reused while
     a graph is being captured."""
-    global _plan_in_workspace
     Nq, Hq, hd = q.shape
     _require(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
              "varlen_attention: bf16 required")
@@ -142,16 +142,17 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     if plan_owner is not None and not torch.cuda.is_current_stream_capturing():
         key = (cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq, max_seqlen_q, Hq, Hkv, ws.data_ptr(),
                ws.numel())
-        if _plan_in_workspace is not None and _plan_in_workspace[0] is plan_owner and _plan_in_workspace[1] == key:
+        cached = _varlen_plans.get(ws.data_ptr())
+        if cached is not None and cached[0] is plan_owner and cached[1] == key:
             plan_stats["reuses"] += 1
         else:
             _lib.check(lib.sd_varlen_plan(cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq, max_seqlen_q,
                                           Hq, Hkv, ws.data_ptr(), ws.numel(), stream), "sd_varlen_plan")
-            _plan_in_workspace = (plan_owner, key)
+            _varlen_plans[ws.data_ptr()] = (plan_owner, key)
             plan_stats["plans"] += 1
         fn = lib.sd_varlen_attention_planned
     else:
-        _plan_in_workspace = None  # the call below rewrites the work lists
+        _varlen_plans.pop(ws.data_ptr(), None)  # the call below rewrites the work lists
     rc = fn(qr.data_ptr(), qr.stride(0), kr.data_ptr(), ks, vr.data_ptr(), vs, total_k, NB, bs, _lib.ptr(block_table), W,
             cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), nseq, Nq, max_seqlen_q, max_seqlen_k, Hq, Hkv, hd,
             scale, out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), stream)

@@ -103,6 +103,30 @@ def test_spec_rows_equal_plain_decode_bitwise(device):
             assert torch.equal(plain.view(B, Hq, D), spec[:, i]), (n, i)
 
 
+@pytest.mark.parametrize("n", [2, 5, 9])
+def test_batch_64_against_batches_of_16_bitwise(device, n):
+    """B = 64 (eight-wave workgroups merging the residues in LDS; at n = 9 three row tiles, merged in two
+    passes, with Q read from LDS) equals the same sequences in batches of 16 (four-wave workgroups, one per
+    CU, partials merged by attn_combine; at n <= 5 two tiles in flight per wave) and plain decode of each
+    row, bitwise."""
+    Hq, Hkv, D, W = 32, 8, 128, 33
+    rnd = random.Random(93 + n)
+    ctx = [rnd.randint(1, 8192) for _ in range(64)]
+    kc, vc, tables = paged_cache(device, ctx, Hkv, D, W=W, seed=93)
+    q = queries(device, 64 * n, Hq, D, seed=94).view(64, n, Hq, D)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+    full = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5)
+    for b0 in range(0, 64, 16):
+        part = paged_decode_attention(q[b0:b0 + 16], kc, vc, lens[b0:b0 + 16], tables[b0:b0 + 16], D ** -0.5)
+        assert torch.equal(part, full[b0 * n:(b0 + 16) * n]), b0
+    spec = full.view(64, n, Hq, D)
+    for i in sorted({0, n // 2, n - 1}):
+        plain = paged_decode_attention(q[:, i:i + 1].contiguous(), kc, vc, (lens - (n - 1 - i)).clamp_min(0), tables,
+                                       D ** -0.5)
+        ok = lens - (n - 1 - i) >= 1   # rows that see at least one key
+        assert torch.equal(plain.view(64, Hq, D)[ok], spec[:, i][ok]), i
+
+
 def test_repeatable_bitwise(device):
     ctx = [random.Random(3).randint(1024, 8192) for _ in range(16)]
     kc, vc, tables = paged_cache(device, ctx, 8, 128, W=33, seed=21)
@@ -163,7 +187,7 @@ def test_planned_order_bitwise_and_stale_plan(device):
         paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5, plan_owner=owner)
         lens.copy_(torch.tensor(ctx, dtype=torch.int32, device=device))
         stale = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5, plan_owner=owner)
-        assert att._decode_plan_in_workspace[0] is owner
+        assert any(plan[0] is owner for plan in att._decode_plans.values())
         assert torch.equal(stale, ref), B
 
 
