@@ -7,11 +7,11 @@
 //   1. row_stats       (row, span): first argmax of the raw logits of target rows; for rows with temperature
 //                      != 0 also max and sum(exp(x - max)) of x = l / T (target rows and, when given, draft
 //                      rows), kept per thread online and combined in a fixed order.
-//   decide_seq         (seq): merges span stats in span order (argmax, logsumexp), applies the accept rule
+//   verify_decide      (seq): merges span stats in span order (argmax, logsumexp), applies the accept rule
 //                      u * q(d) < p(d) (or top1 == d for greedy rows) to the leading run of real guesses,
-//                      writes num_accepted and, for greedy rows, next_token. It runs as its own kernel
-//                      (verify_decide) when every row is greedy, else in the prologue of every resample
-//                      workgroup of the sequence.
+//                      writes num_accepted, for greedy rows next_token, and the sequence's decision for the
+//                      resample. (Taking the decision in the prologue of every resample workgroup instead
+//                      cost as much as this launch: the resample's loads then wait for it.)
 //   2. verify_resample (seq, span): random rows only, over up to 64 spans per row (a single row per
 //                      sequence: more spans keep a small batch spread over the GPU): the first argmax of
 //                      p / max(E, 1e-10) and of residual / max(E, 1e-10) with p = softmax(row a / T), residual =
@@ -39,7 +39,7 @@ constexpr int kThreads = 256;
 struct RowStat {                  // per (row, chunk)
   float max_x;                    // max of l / T over the chunk (random rows; -inf for an all -inf chunk)
   float sum;                      // sum of exp(l / T - lse_shift(max_x)) (random rows)
-  float best;                     // raw logit at the chunk's first argmax (target rows)
+  float best;                     // raw logit at the chunk's first argmax (greedy target rows)
   int32_t best_idx;
 };
 
@@ -316,15 +316,17 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
   OnlineSum os;
   const float z = random ? 1.f / T : 1.f;
   if (is_target) {
+    // The first argmax matters for greedy rows only (the decision and the next token of a sampled row use
+    // the softmax statistics and the noise): sampled rows skip it.
     const void* base = DT == SD_DTYPE_F32
                            ? (const void*)((const float*)p.logits + (int64_t)row * p.logits_stride)
                            : (const void*)((const uint16_t*)p.logits + (int64_t)row * p.logits_stride);
     if (!random)
       scan_span<DT, kVec, true, false, false>(base, v0, v1, T, z, bv, bi, os);
     else if (T == 1.f)
-      scan_span<DT, kVec, true, true, false>(base, v0, v1, T, z, bv, bi, os);
+      scan_span<DT, kVec, false, true, false>(base, v0, v1, T, z, bv, bi, os);
     else
-      scan_span<DT, kVec, true, true, true>(base, v0, v1, T, z, bv, bi, os);
+      scan_span<DT, kVec, false, true, true>(base, v0, v1, T, z, bv, bi, os);
   } else {
     const int64_t dr = row - target_rows;
     const void* base = DDT == SD_DTYPE_F32 ? (const void*)((const float*)p.draft_logits + dr * p.draft_stride)
@@ -337,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void row_stats(VParams p) {
   RowStat st;
   st.max_x = -INFINITY;
   st.sum = 0.f;
-  if (is_target) block_argmax(bv, bi, shf, shi);
+  if (is_target && !random) block_argmax(bv, bi, shf, shi);
   st.best = bv;
   st.best_idx = bi;
   if (random) {
@@ -363,19 +365,18 @@ __device__ void merge_softmax(const RowStat* st, int nchunk, float* shift_out, f
   *S_out = s;
 }
 
-// The decision for one sequence, by one workgroup (any size from 64 threads; every thread must call it). Every
-// global read is issued up front (the span statistics of the sequence's rows into LDS; per guess slot the guess,
-// its uniform and its target and draft logits), then lane j merges row j's spans and evaluates guess j, and the
-// leading run of accepts gives a. With `publish`, thread 0 writes num_accepted, the greedy token and the
-// sequence's SeqInfo. Returns that SeqInfo to every thread.
+// The decision for one sequence, by one workgroup of 64 threads. Every global read is issued up front (the
+// span statistics of the sequence's rows into LDS; per guess slot the guess, its uniform and its target and
+// draft logits), then lane j merges row j's spans and evaluates guess j, and the leading run of accepts gives
+// a. Thread 0 writes num_accepted, the greedy token and the sequence's SeqInfo.
 template <int DT, int DDT, bool kRand>
-__device__ SeqInfo decide_seq(const VParams& p, int seq, bool publish) {
+__global__ __launch_bounds__(64) void verify_decide(VParams p) {
+  const int seq = blockIdx.x;
   __shared__ RowStat sst[(64 + 63) * kSpans];
   __shared__ int32_t top1[64];
   __shared__ float lse[64], dlse[64], tshift[64], tsum[64], dshift[64], dsum[64];
   __shared__ int accj[64];
   __shared__ int64_t guess[64];
-  __shared__ SeqInfo shared_info;
   const int lane = threadIdx.x;
   const int nthr = blockDim.x;
   const int K = p.K, nchunk = p.nchunk;
@@ -464,21 +465,10 @@ __device__ SeqInfo decide_seq(const VParams& p, int seq, bool publish) {
         }
       }
     }
-    shared_info = info;
-    if (publish) {
-      p.out_a[seq] = a;
-      if (!random) p.out_next[seq] = top1[a];
-      p.info[seq] = info;
-    }
+    p.out_a[seq] = a;
+    if (!random) p.out_next[seq] = top1[a];
+    p.info[seq] = info;
   }
-  __syncthreads();
-  return shared_info;
-}
-
-// The decision alone, one 64-lane workgroup per sequence (the all-greedy path, where no resampling follows).
-template <int DT, int DDT, bool kRand>
-__global__ __launch_bounds__(64) void verify_decide(VParams p) {
-  decide_seq<DT, DDT, kRand>(p, blockIdx.x, true);
 }
 
 // One workgroup per random sequence: thread k reads span k's candidate (all reads in flight together),
@@ -536,9 +526,7 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
   __shared__ int shi[4];
   const int seq = blockIdx.x;
   const int chunk = blockIdx.y;
-  // Every span's workgroup takes the sequence's decision itself (the statistics are a few KB); span 0's
-  // publishes it.
-  const SeqInfo info = decide_seq<DT, DDT, true>(p, seq, chunk == 0);
+  const SeqInfo info = p.info[seq];  // verify_decide's
   if (!info.random) return;
   const float T = p.temps[seq];
   const bool div = T != 1.f;
@@ -641,10 +629,10 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
       }
     }
   };
-  // Per lane: the entry with the largest upper bound (with its values) and the second-largest upper bound.
+  // Per lane: the entry with the largest upper bound and the second-largest upper bound (the entry's values
+  // are read again for its exact evaluation).
   float b1p = -INFINITY, b2p = -INFINITY, b1r = -INFINITY, b2r = -INFINITY, lr = -INFINITY;
   int i1p = -1, i1r = -1;
-  float cp[3] = {0.f, 0.f, 0.f}, cr[3] = {0.f, 0.f, 0.f};
   bool sure = false, odd = false;
   sweep([&](int i, float l, float E, float ld) {
     const Bounds b = bounds(i, l, E, ld);
@@ -653,7 +641,6 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
       b2p = b1p;
       b1p = b.ubp;
       i1p = i;
-      cp[0] = l, cp[1] = E, cp[2] = ld;
     } else {
       b2p = fmaxf(b2p, b.ubp);
     }
@@ -662,7 +649,6 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
         b2r = b1r;
         b1r = b.ubr;
         i1r = i;
-        cr[0] = l, cr[1] = E, cr[2] = ld;
       } else {
         b2r = fmaxf(b2r, b.ubr);
       }
@@ -679,8 +665,8 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
   const bool rescan = odd || tiny_p || tiny_r || (resid && !sure_any) || b2p >= Lp || (resid && b2r >= Lr);
   if (!rescan) {
     const bool ep = i1p >= 0 && b1p >= Lp;
-    if (ep) exact(i1p, cp[0], cp[1], cp[2]);
-    if (resid && i1r >= 0 && b1r >= Lr && !(ep && i1r == i1p)) exact(i1r, cr[0], cr[1], cr[2]);
+    if (ep) reload(i1p);
+    if (resid && i1r >= 0 && b1r >= Lr && !(ep && i1r == i1p)) reload(i1r);
   } else {
     sweep([&](int i, float l, float E, float ld) {
       const Bounds b = bounds(i, l, E, ld);
@@ -736,7 +722,8 @@ VLayout verify_layout(int S, int K, int V, bool draft) {
   return L;
 }
 
-// Greedy-only calls (no temperatures) run the argmax pass and the decision alone.
+// Greedy-only calls (no temperatures) run the argmax pass and the decision alone; sampled calls then resample
+// the sampled sequences and pick their tokens.
 template <int DT, int DDT, bool kVec>
 int launch_all(const VParams& p, hipStream_t s, bool draft) {
   int rc;
@@ -749,6 +736,8 @@ int launch_all(const VParams& p, hipStream_t s, bool draft) {
   const int rows = p.S * (p.K + 1) + (draft ? p.S * p.K : 0);
   hipLaunchKernelGGL((row_stats<DT, DDT, kVec, true>), dim3(rows, p.nchunk), dim3(kThreads), 0, s, p);
   if ((rc = check_launch("row_stats"))) return rc;
+  hipLaunchKernelGGL((verify_decide<DT, DDT, true>), dim3(p.S), dim3(64), 0, s, p);
+  if ((rc = check_launch("verify_decide"))) return rc;
   hipLaunchKernelGGL((verify_resample<DT, DDT, kVec>), dim3(p.S, p.rchunk), dim3(kThreads), 0, s, p);
   if ((rc = check_launch("verify_resample"))) return rc;
   hipLaunchKernelGGL(verify_finish, dim3(p.S), dim3(kThreads), 0, s, p);
@@ -823,7 +812,7 @@ int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_
 // ---- LM head + verifier ----
 
 // The first argmax of each token row over the LM head's per-workgroup results, into the span statistics of
-// a one-span row (decide_seq reads them); one wave per row, any tree order (the argmax order is total).
+// a one-span row (verify_decide reads them); one wave per row, any tree order (the argmax order is total).
 __global__ __launch_bounds__(64) void lm_head_merge(const lmhead::TileBest* best, int tiles, RowStat* stats) {
   const int m = blockIdx.x;
   float bv = -INFINITY;
