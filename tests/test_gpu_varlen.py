@@ -126,6 +126,50 @@ def test_prefill_rows_chunk_invariant_bitwise(device):
     _check(whole, ref, "700-token prefill")
 
 
+@pytest.mark.parametrize("paged", [True, False])
+def test_prefill_only_and_mixed_calls_agree_bitwise(device, paged):
+    """A call with prefill chunks only and the same chunks beside a 5-query sequence (a mixed launch, whose
+    residue items share the grid) give bitwise equal prefill rows: chunks of 1000 queries after 1100 cached
+    keys (q-blocks across the causal diagonal), 37 and 300 queries (partial q-blocks), fresh or paged keys."""
+    Hq, Hkv, D = 32, 8, 128
+    lq, lk = [1000, 37, 300], [2100, 37, 300]
+    if paged:
+        kc, vc, tables = paged_cache(device, lk + [lk[0]], Hkv, D, seed=21)
+        k = v = None
+    else:
+        g = torch.Generator(device=device).manual_seed(21)
+        k = torch.randn(sum(lk) + lk[0], Hkv, D, device=device, generator=g).to(torch.bfloat16)
+        v = torch.randn(sum(lk) + lk[0], Hkv, D, device=device, generator=g).to(torch.bfloat16)
+    q = queries(device, sum(lq) + 5, Hq, D, seed=22)
+
+    # sequence j's keys: table row j (paged), or rows off[j] .. off[j] + lk[j] of k / v; sequence 3 (the
+    # 5-query one) has chunk 0's key count in its own rows
+    lens = lk + [lk[0]]
+    off = np.cumsum([0] + lens).tolist()
+
+    def run(lq_, seqs, qrows):
+        lk_ = [lens[j] for j in seqs]
+        if paged:
+            return varlen_attention(qrows, kc, vc, _cu(lq_, device), _cu(lk_, device), max(lq_), max(lk_),
+                                    D ** -0.5, tables[seqs])
+        keys = torch.cat([k[off[j]:off[j] + lens[j]] for j in seqs])
+        vals = torch.cat([v[off[j]:off[j] + lens[j]] for j in seqs])
+        return varlen_attention(qrows, keys, vals, _cu(lq_, device), _cu(lk_, device), max(lq_), max(lk_),
+                                D ** -0.5)
+
+    alone = run(lq, [0, 1, 2], q[:sum(lq)])
+    mixed = run([5] + lq, [3, 0, 1, 2], torch.cat([q[sum(lq):], q[:sum(lq)]]))
+    assert torch.equal(mixed[5:], alone)
+    lq_cpu, lk_cpu = _cu(lq, "cpu"), _cu(lk, "cpu")
+    if paged:
+        ref = oatt.varlen_attention(q[:sum(lq)].cpu(), kc.cpu(), vc.cpu(), lq_cpu, lk_cpu, D ** -0.5,
+                                    tables[[0, 1, 2]].cpu())
+    else:
+        ref = oatt.varlen_attention(q[:sum(lq)].cpu(), k[:sum(lk)].cpu(), v[:sum(lk)].cpu(), lq_cpu, lk_cpu,
+                                    D ** -0.5)
+    _check(alone, ref, f"prefill-only call ({'paged' if paged else 'fresh'} keys)")
+
+
 def test_plan_reuse_across_layers(device):
     """The step's work lists are planned once per owner (the step's Context) and reused by later layers:
     bitwise equal to unplanned calls; a different owner replans, and so does the first owner afterwards
