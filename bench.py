@@ -476,8 +476,8 @@ def bench_mixed_step_full(dev, layers=36, steps=5, warmup=2):
     MLP 12288, vocab 151936, bf16) run piecewise by the mixed-step runtime in one HIP graph per bucket
     (embedding, per layer: input norm + qkv GEMM, fused q/k norm + RoPE + KV store, varlen attention,
     o_proj + post norm + MLP; final norm), then, eagerly as the reference's run_mixed does, the LM head on the
-    step's logits rows and the greedy verifier on the decode rows. Reports the model step alone (graph replay)
-    and the whole step, as query tokens per second."""
+    decode requests' verify rows and the greedy verifier (sd_lm_head_verify: one call, no logits written).
+    Reports the model step alone (graph replay) and the whole step, as query tokens per second."""
     import torch
     from types import SimpleNamespace
     from nanovllm_amd import _lib
@@ -506,18 +506,22 @@ def bench_mixed_step_full(dev, layers=36, steps=5, warmup=2):
     acc = torch.empty(nd, dtype=torch.int64, device=dev)
     nxt = torch.empty(nd, dtype=torch.int64, device=dev)
     V = 151936
-    ws = torch.empty(lib.sd_verify_workspace_size(nd, K, V, 0), dtype=torch.uint8, device=dev)
+    from nanovllm_amd.layers.lm_head import pack_weight
+    wp = pack_weight(seg.lm_head)   # once per model
+    H = seg.hidden
+    ws = torch.empty(lib.sd_lm_head_verify_workspace_size(nd, K, V, H, 0), dtype=torch.uint8, device=dev)
 
     def model_step():
         runner.run(layout)
 
     def whole_step():
+        # the step, then the LM head over the decode requests' verify rows and the greedy verifier in one call
         runner.run(layout)
-        logits = seg.logits(seg.hidden_out.index_select(0, idx))
-        _lib.check(lib.sd_verify_drafts(logits.data_ptr(), _lib.DTYPE_BF16, V, drafts.data_ptr(), ndr.data_ptr(),
-                                        None, None, 0, 0, None, None, nd, K, V, acc.data_ptr(), nxt.data_ptr(),
-                                        ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream),
-                   "sd_verify_drafts")
+        h = seg.hidden_out
+        _lib.check(lib.sd_lm_head_verify(h.data_ptr(), h.stride(0), h.size(0), idx.data_ptr(), wp.data_ptr(), V, H,
+                                         drafts.data_ptr(), ndr.data_ptr(), None, None, 0, 0, None, None, nd, K, None,
+                                         0, acc.data_ptr(), nxt.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         torch.cuda.current_stream().cuda_stream), "sd_lm_head_verify")
 
     wall_m, _ = timed(model_step, steps, warmup)
     wall_w, _ = timed(whole_step, steps, warmup)
@@ -527,8 +531,8 @@ def bench_mixed_step_full(dev, layers=36, steps=5, warmup=2):
                query_tokens=n, bucket_tokens=N, logits_rows=len(layout["logits_indices"]),
                layer_gemm_tflops_per_step=round(gemm_flops / 1e12, 2),
                timing="wall clock of back-to-back steps between synchronizations (the step's metadata copy, "
-                      "one graph replay, then the LM head and the verifier eagerly)")
-    del caches, kc, vc, seg, runner
+                      "one graph replay, then sd_lm_head_verify eagerly)")
+    del caches, kc, vc, seg, runner, wp
     torch.cuda.empty_cache()
     return res
 
