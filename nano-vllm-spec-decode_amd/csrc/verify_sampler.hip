@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "lm_head.h"
 #include "sd_common.h"
@@ -584,24 +585,33 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
     float ubp, ubr, lbr;
     bool live, sure;
   };
-  auto bounds = [&](int i, float l, float E, float ld) {
+  // Specialised by mode (residual or not, division by T or not), so that the first pass has no per-entry
+  // branch; with noise absent E is 1 and max(E, 1e-10) is 1.
+  auto bounds_t = [&](auto resid_c, auto div_c, int i, float l, float E, float ld) {
 #pragma clang fp contract(off)
+    constexpr bool kR = decltype(resid_c)::value, kD = decltype(div_c)::value;
     Bounds b;
-    const float rE = __builtin_amdgcn_rcpf(noise ? fmaxf(E, 1e-10f) : 1.f);
-    const float dp = (div ? l * z : l) - info.Ma;
-    const float pa = i == zap ? 0.f : exp2_fast(fmaf(dp, kL2E, lsa));
+    const float rE = __builtin_amdgcn_rcpf(fmaxf(E, 1e-10f));
+    const float dp = (kD ? l * z : l) - info.Ma;
+    const float pa = !kR && i == zap ? 0.f : exp2_fast(fmaf(dp, kL2E, lsa));  // zap is -1 in residual mode
     b.live = dp > kUnderflow;
     b.ubp = pa * rE * up;
     b.ubr = b.lbr = 0.f;
     b.sure = false;
-    if (resid) {
-      const float qa = exp2_fast(fmaf((div ? ld * z : ld) - info.Md, kL2E, lsd));
+    if constexpr (kR) {
+      const float qa = exp2_fast(fmaf((kD ? ld * z : ld) - info.Md, kL2E, lsd));
       const float slack = 2.f * eps * (pa + qa);
       b.ubr = (fmaxf(pa - qa, 0.f) + slack) * rE * up;
       b.lbr = fmaxf(pa - qa - slack, 0.f) * rE * dn;
       b.sure = pa - qa - slack > 0.f;
     }
     return b;
+  };
+  using True_ = std::true_type;
+  using False_ = std::false_type;
+  auto bounds = [&](int i, float l, float E, float ld) {
+    if (resid) return div ? bounds_t(True_{}, True_{}, i, l, E, ld) : bounds_t(True_{}, False_{}, i, l, E, ld);
+    return div ? bounds_t(False_{}, True_{}, i, l, E, ld) : bounds_t(False_{}, False_{}, i, l, E, ld);
   };
   // Pass over the span, in rounds of 8 entries a lane (v .. v+3 and v+kStep .. v+kStep+3).
   constexpr int kStep = 4 * kThreads;
@@ -634,28 +644,33 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
   float b1p = -INFINITY, b2p = -INFINITY, b1r = -INFINITY, b2r = -INFINITY, lr = -INFINITY;
   int i1p = -1, i1r = -1;
   bool sure = false, odd = false;
-  sweep([&](int i, float l, float E, float ld) {
-    const Bounds b = bounds(i, l, E, ld);
-    odd = odd || b.ubp != b.ubp || b.ubr != b.ubr;
-    if (b.ubp > b1p) {
-      b2p = b1p;
-      b1p = b.ubp;
-      i1p = i;
-    } else {
-      b2p = fmaxf(b2p, b.ubp);
-    }
-    if (resid) {
-      if (b.ubr > b1r) {
-        b2r = b1r;
-        b1r = b.ubr;
-        i1r = i;
-      } else {
-        b2r = fmaxf(b2r, b.ubr);
+  // Branch-free updates (selects, which keep the running value where an entry is NaN, as fmaxf does): early
+  // in the span nearly every entry is some lane's new best, so a branch would run the update code for the
+  // whole wave anyway. One instantiation per mode.
+  auto first_pass = [&](auto resid_c, auto div_c) {
+    constexpr bool kR = decltype(resid_c)::value;
+    sweep([&](int i, float l, float E, float ld) {
+      const Bounds b = bounds_t(resid_c, div_c, i, l, E, ld);
+      odd = odd || b.ubp != b.ubp || (kR && b.ubr != b.ubr);
+      const bool np = b.ubp > b1p;
+      b2p = np ? b1p : (b.ubp > b2p ? b.ubp : b2p);
+      i1p = np ? i : i1p;
+      b1p = np ? b.ubp : b1p;
+      if constexpr (kR) {
+        const bool nr = b.ubr > b1r;
+        b2r = nr ? b1r : (b.ubr > b2r ? b.ubr : b2r);
+        i1r = nr ? i : i1r;
+        b1r = nr ? b.ubr : b1r;
+        lr = b.lbr > lr ? b.lbr : lr;
+        sure = sure || b.sure;
       }
-      lr = fmaxf(lr, b.lbr);
-      sure = sure || b.sure;
-    }
-  });
+    });
+  };
+  if (resid) {
+    if (div) first_pass(True_{}, True_{}); else first_pass(True_{}, False_{});
+  } else {
+    if (div) first_pass(False_{}, True_{}); else first_pass(False_{}, False_{});
+  }
   // The largest lower bound of p / E in the span: the largest upper bound scaled down, less one rounding.
   const float Lp = block_max(b1p, shf) * (dn / up) * (1.f - 2.384185791015625e-07f);
   const float Lr = resid ? block_max(lr, shf + 4) : 0.f;
