@@ -43,7 +43,8 @@ class Qwen3Segments:
 
     Buffers (fixed addresses, max_tokens rows): input_ids int64 (the caller writes a step's token ids, 0 for
     padding rows, before the runner's run), residual and hidden bf16 [max_tokens, hidden]; after a step,
-    hidden[:n] holds the final-norm hidden states and logits(rows) applies the LM head."""
+    hidden_out[:n] holds the final-norm hidden states, to which the caller applies the LM head `lm_head`
+    (with the verifier: nanovllm_amd.layers.lm_head.LMHeadVerifier(seg.lm_head))."""
 
     def __init__(self, num_layers: int = 36, hidden: int = 4096, num_heads: int = 32, num_kv_heads: int = 8,
                  head_dim: int = 128, intermediate: int = 12288, vocab: int = 151936, eps: float = 1e-6,
@@ -96,7 +97,3 @@ class Qwen3Segments:
             x, residual = add_rms_norm(h, residual, self.layers[i]["in_norm"], self.eps)
         self.residual[:n] = residual
         torch.mm(x, self.layers[i]["qkv"].t(), out=bufs["qkv"][:n])
-
-    def logits(self, rows: torch.Tensor) -> torch.Tensor:
-        """ParallelLMHead.forward on already gathered rows (nanovllm/layers/embed_head.py:56-68, one rank)."""
-        return F.linear(rows, self.lm_head)

@@ -46,8 +46,11 @@ def test_workspace_sizes(lib):
     assert lib.sd_paged_decode_workspace_size(63, 5, 32, 8, 128, 256, 33) == 256
     # 16 sequences: residue partials [16 items][8 heads][8 residues][32 rows] x (128 + 2) fp32
     assert lib.sd_paged_decode_workspace_size(16, 5, 32, 8, 128, 256, 33) >= 16 * 8 * 8 * 32 * 130 * 4
-    # 9 queries x 4 heads = 36 rows -> 3 row tiles, which never merge in LDS
-    assert lib.sd_paged_decode_workspace_size(64, 9, 32, 8, 128, 256, 33) >= 64 * 8 * 8 * 48 * 130 * 4
+    # 9 queries x 4 heads = 36 rows -> 3 row tiles: merged in LDS at 64 sequences, partials at 16
+    assert lib.sd_paged_decode_workspace_size(64, 9, 32, 8, 128, 256, 33) == 512
+    assert lib.sd_paged_decode_workspace_size(16, 9, 32, 8, 128, 256, 33) >= 16 * 8 * 8 * 48 * 130 * 4
+    # 17 queries x 4 heads = 68 rows -> 4 row tiles (64 rows) in two query groups, never merged in LDS
+    assert lib.sd_paged_decode_workspace_size(64, 17, 32, 8, 128, 256, 33) >= 128 * 8 * 8 * 64 * 130 * 4
     assert lib.sd_paged_decode_workspace_size(0, 5, 32, 8, 128, 256, 33) == 0
     assert lib.sd_varlen_workspace_size(51, 2048, 4096, 32, 8, 128) > 0
     # per-row statistics of 8 spans (16 B each) for 64 x 5 target and 64 x 4 draft rows
