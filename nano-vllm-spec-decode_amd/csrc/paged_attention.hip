@@ -49,7 +49,8 @@ constexpr int kResidues = 8;                   // tile t belongs to residue t % 
 constexpr int kVBuf = kTile * kD * 2;          // one 32-key V tile in LDS: 8 KB per wave
 constexpr int kObRow = kD + 4;                 // fp32 row stride of the merge buffer (bank padding)
 constexpr int kMaxRows = 64;                   // 16-row tiles: at most 4
-constexpr int kMaxBlocks = 1024;               // block-table entries staged in LDS per item
+constexpr int kMaxBlocks = 2048;               // block-table entries staged in LDS per item (64 K keys at block
+                                               // size 32, 512 K at 256)
 constexpr int kMlBytes = kResidues * kMaxRows * 2 * 4;
 constexpr int kMergeRows = 32;                 // rows merged in LDS per pass (two row tiles)
 constexpr int kObBytes = kResidues * kMergeRows * kObRow * 4;

@@ -75,7 +75,7 @@ constexpr int kThreads = kWaves * kWave;               // 512
 constexpr int kTileBytes = kTile * kD * 2;             // one K or V tile: 8 KB
 constexpr int kStageBytesMax = 2 * 2 * kTileBytes;     // [parity][K, V] with two parities: 32 KB
 constexpr int kStages = 2;                             // LDS stage buffers
-constexpr int kMaxBlocks = 1024;                       // block-table entries staged in LDS
+constexpr int kMaxBlocks = 2048;                       // block-table entries staged in LDS
 constexpr float kLazyLog2 = 8.f;                       // rescale threshold (exp2 domain)
 constexpr int kLdsBytes = kStages * kStageBytesMax + kMaxBlocks * 4 + kWaves * 4;  // + per-wave flags
 // The parity merge (two parities, four row groups) reuses the stage buffers and the block ids: O of the four
@@ -144,9 +144,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   int32_t* blk_ids = (int32_t*)(lds + kStages * kStageBytesMax);
   const int nblk_row = min(p.table_width, kMaxBlocks);
   const int nb_used = kPaged ? min((kmax + p.block_size - 1) / p.block_size, nblk_row) : 0;
-  int32_t blk_pre[2];
+  constexpr int kBlkPer = kMaxBlocks / kThreads;
+  int32_t blk_pre[kBlkPer];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kBlkPer; ++i) {
     const int b = tid + i * kThreads;
     blk_pre[i] = b < nb_used ? p.block_tables[(int64_t)seq * p.table_width + b] : 0;
   }
@@ -168,14 +169,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
   wait_vm_all();  // Q and block ids in registers before any stage load is issued
   bool bad = false;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kBlkPer; ++i) {
     const int b = tid + i * kThreads;
     if (b < nb_used) {
       blk_ids[b] = blk_pre[i];
       bad |= blk_pre[i] < 0 || blk_pre[i] >= p.num_blocks;
     }
   }
-  static_assert(2 * kThreads >= kMaxBlocks, "two block ids per thread");
+  static_assert(kBlkPer * kThreads == kMaxBlocks, "block ids per thread");
   int32_t* bad_flags = blk_ids + kMaxBlocks;  // one per wave: the wave staged an invalid block id
   const int wave_bad = __any(bad);
   if (lane == 0) bad_flags[wave] = wave_bad;

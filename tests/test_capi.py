@@ -67,6 +67,9 @@ def test_bad_arguments_return_status(lib):
     rc = lib.sd_paged_decode(None, 4096, None, None, 10, 100, None, None, 4, 2, 5, 32, 8, 128, 0.1, None, 4096,
                              None, 0, None)
     assert rc == 2 and b"block_size" in lib.sd_last_error()
+    rc = lib.sd_paged_decode(None, 4096, None, None, 10, 32, None, None, 2049, 2, 5, 32, 8, 128, 0.1, None, 4096,
+                             None, 0, None)
+    assert rc == 2 and b"table width 2049 exceeds 2048" in lib.sd_last_error()
     rc = lib.sd_varlen_attention(None, 4096, None, 1024, None, 1024, 0, 0, 0, None, 0, None, None, 1, 10, 10, 10,
                                  30, 8, 128, 0.1, None, 4096, None, 0, None)
     assert rc == 1 and b"multiple" in lib.sd_last_error()

@@ -57,3 +57,50 @@ def test_varlen_block_sizes_and_head_ratios(device, bs, Hq, Hkv):
     out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
     ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
     _check(out, ref, f"varlen bs={bs} Hq={Hq} Hkv={Hkv}")
+
+
+def _aliased_cache(device, B, W, Hkv, bs, NB=48, seed=0):
+    """A small cache of NB blocks behind block tables of width W whose entries alias them at random: contexts
+    of W * bs keys without W * B blocks of memory."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    kc = torch.randn(NB, bs, Hkv, D, device=device, generator=g).to(torch.bfloat16)
+    vc = torch.randn(NB, bs, Hkv, D, device=device, generator=g).to(torch.bfloat16)
+    tables = torch.randint(0, NB, (B, W), device=device, generator=g, dtype=torch.int32)
+    return kc, vc, tables
+
+
+@pytest.mark.parametrize("B", [2, 16, 64])
+def test_decode_tables_past_1024_blocks(device, B):
+    """Block size 32 with contexts of 33-36 K keys: tables of 1130 blocks, more than half the 2048 block ids a
+    work item stages in LDS (B = 2: the one-residue stream kernel, 16: four-wave workgroups with partials,
+    64: eight-wave workgroups merging in LDS)."""
+    bs, Hq, Hkv, n, W = 32, 32, 8, 5, 1130
+    kc, vc, tables = _aliased_cache(device, B, W, Hkv, bs, seed=B)
+    rnd = np.random.default_rng(B)
+    ctx = rnd.integers(33000, W * bs + 1, B).tolist()
+    q = queries(device, B * n, Hq, D, seed=B + 1).view(B, n, Hq, D)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+    out = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5)
+    rows = list(range(min(B, 4)))   # the oracle on a few sequences
+    ref = oatt.paged_decode_attention(q[rows].cpu(), kc.cpu(), vc.cpu(), lens[rows].cpu(), tables[rows].cpu(),
+                                      D ** -0.5)
+    _check(out.view(B, n, Hq, D)[rows], ref, f"B={B}, tables of {W} blocks")
+
+
+def test_varlen_tables_past_1024_blocks(device):
+    """A 40-query prefill chunk after 34 000 cached keys and a 5-query verify row over 35 000 keys, block size
+    32 (1130-block tables), in one mixed launch and as a prefill-only call."""
+    bs, Hq, Hkv, W = 32, 32, 8, 1130
+    kc, vc, tables = _aliased_cache(device, 2, W, Hkv, bs, seed=7)
+    lq, lk = [5, 40], [35000, 34040]
+    q = queries(device, sum(lq), Hq, D, seed=8)
+    cu_q = torch.tensor([0, 5, 45], dtype=torch.int32, device=device)
+    cu_k = torch.tensor([0, lk[0], lk[0] + lk[1]], dtype=torch.int32, device=device)
+    out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
+    ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
+    _check(out, ref, "varlen, tables of 1130 blocks")
+    # the chunk alone (a prefill-only call) gives the same rows bitwise
+    cu_q1 = torch.tensor([0, lq[1]], dtype=torch.int32, device=device)
+    cu_k1 = torch.tensor([0, lk[1]], dtype=torch.int32, device=device)
+    alone = varlen_attention(q[5:], kc, vc, cu_q1, cu_k1, lq[1], lk[1], D ** -0.5, tables[1:])
+    assert torch.equal(alone, out[5:])
