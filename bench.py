@@ -317,11 +317,11 @@ def bench_sampler(dev, steps, warmup, S=64, K=4, V=151936):
                 V if with_draft else 0, u.data_ptr() if T else None, e.data_ptr() if T else None, S, K, V,
                 acc.data_ptr(), nxt.data_ptr(), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream),
                 "sd_verify_drafts")
-        t = graph_timed(call, reps=10)
+        t = graph_timed(call, reps=10, replays=20)
         nbytes = S * (K + 1) * V * 4 + ((S * K * V * 4 + 2 * S * V * 4 + S * V * 4) if T else 0)
         res[f"T{int(T)}"] = dict(us=round(t * 1e6, 2), GBs=round(nbytes / t / 1e9, 1),
                                  frac=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), bytes=nbytes,
-                                 timing="graph replay of 10 calls")
+                                 timing="20 graph replays of 10 calls")
     return res
 
 

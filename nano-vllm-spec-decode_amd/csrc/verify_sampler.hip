@@ -35,6 +35,7 @@ namespace sd {
 namespace {
 
 constexpr int kSpans = 8;         // most spans per row (workgroups per row)
+constexpr int kPipeU = 2;         // verify_resample: 4-entry groups a lane loads per pipeline stage
 constexpr int kThreads = 256;
 
 struct RowStat {                  // per (row, chunk)
@@ -481,8 +482,8 @@ __global__ __launch_bounds__(kThreads) void verify_finish(VParams p) {
   __shared__ float shf[4];
   __shared__ int shi[4];
   const int seq = blockIdx.x;
-  const SeqInfo info = p.info[seq];
-  if (!info.random) return;
+  // The candidates are read with the decision (both in flight together); a greedy sequence has no
+  // candidates (stale workspace), and its workgroup returns before using them.
   float pv = -INFINITY, rv = -INFINITY;
   int pi = 0x7fffffff, ri = 0x7fffffff, any_res = 0;
   for (int k = threadIdx.x; k < p.rchunk; k += kThreads) {
@@ -497,6 +498,8 @@ __global__ __launch_bounds__(kThreads) void verify_finish(VParams p) {
     }
     any_res |= c.any_res;
   }
+  const SeqInfo info = p.info[seq];
+  if (!info.random) return;
   block_argmax(pv, pi, shf, shi);
   block_argmax(rv, ri, shf, shi);
   any_res = __syncthreads_or(any_res);
@@ -527,9 +530,9 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
   __shared__ int shi[4];
   const int seq = blockIdx.x;
   const int chunk = blockIdx.y;
+  const float T = p.temps[seq];
   const SeqInfo info = p.info[seq];  // verify_decide's
   if (!info.random) return;
-  const float T = p.temps[seq];
   const bool div = T != 1.f;
   const float z = 1.f / T;
   const int K = p.K;
@@ -647,9 +650,57 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
   // Branch-free updates (selects, which keep the running value where an entry is NaN, as fmaxf does): early
   // in the span nearly every entry is some lane's new best, so a branch would run the update code for the
   // whole wave anyway. One instantiation per mode.
+  // The first pass over aligned rows with noise, software-pipelined: the loads of a lane's next kPipeU groups
+  // of 4 entries are in flight while the current ones are screened (two register buffers, used in turn, so
+  // that no copy waits for loads). Aligned noise rows make the vocabulary a multiple of 4, so a span is whole
+  // 4-entry groups; addresses past the span's end are clamped to its last group and those entries skipped.
+  struct Stage {
+    float4 t[kPipeU], e[kPipeU], d[kPipeU];
+  };
+  constexpr int kStage = kPipeU * kStep;
+  const int stages = (v1 - v0 + kStage - 1) / kStage;
+  auto pipe = [&](auto resid_c, auto&& visit) {
+    constexpr bool kR = decltype(resid_c)::value;
+    auto load = [&](int g, Stage& st) {
+#pragma unroll
+      for (int u = 0; u < kPipeU; ++u) {
+        const int v = min(v0 + g * kStage + u * kStep + 4 * (int)threadIdx.x, v1 - 4);
+        st.t[u] = load_logit4<DT>(tbase, v);
+        st.e[u] = *(const float4*)(noise + v);
+        if (kR) st.d[u] = load_logit4<DDT>(dbase, v);
+      }
+    };
+    auto run = [&](int g, const Stage& st) {
+#pragma unroll
+      for (int u = 0; u < kPipeU; ++u) {
+        const int v = v0 + g * kStage + u * kStep + 4 * threadIdx.x;
+        if (v < v1) {
+          const float4 d4 = kR ? st.d[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+          visit(v, st.t[u].x, st.e[u].x, d4.x);
+          visit(v + 1, st.t[u].y, st.e[u].y, d4.y);
+          visit(v + 2, st.t[u].z, st.e[u].z, d4.z);
+          visit(v + 3, st.t[u].w, st.e[u].w, d4.w);
+        }
+      }
+    };
+    Stage a, b;
+    load(0, a);
+    for (int g = 0; g < stages; g += 2) {
+      load(g + 1, b);
+      run(g, a);
+      load(g + 2, a);
+      run(g + 1, b);
+    }
+  };
   auto first_pass = [&](auto resid_c, auto div_c) {
     constexpr bool kR = decltype(resid_c)::value;
-    sweep([&](int i, float l, float E, float ld) {
+    auto scan = [&](auto&& visit) {
+      if constexpr (kVec) {
+        if (noise) return pipe(resid_c, visit);
+      }
+      sweep(visit);
+    };
+    scan([&](int i, float l, float E, float ld) {
       const Bounds b = bounds_t(resid_c, div_c, i, l, E, ld);
       odd = odd || b.ubp != b.ubp || (kR && b.ubr != b.ubr);
       const bool np = b.ubp > b1p;
@@ -719,9 +770,10 @@ void spans_of(int V, int most, int* nchunk, int* span) {
 // row_stats: at most kSpans per row (the table has S*(K+1) or more rows).
 void row_spans(int V, int* nchunk, int* span) { spans_of(V, kSpans, nchunk, span); }
 // verify_resample reads one target row per sequence (plus its draft row and noise): more spans per row, up
-// to about 2048 workgroups in all, so that a small batch still spreads over the GPU.
+// to about 1024 workgroups in all (4 waves a SIMD, all resident at the pipelined pass's register count), so
+// that a small batch still spreads over the GPU.
 void resample_spans(int S, int V, int* nchunk, int* span) {
-  spans_of(V, std::min(64, std::max(kSpans, (2048 + S - 1) / S)), nchunk, span);
+  spans_of(V, std::min(64, std::max(kSpans, (1024 + S - 1) / S)), nchunk, span);
 }
 
 VLayout verify_layout(int S, int K, int V, bool draft) {
