@@ -3,7 +3,8 @@
     python nano-vllm-spec-decode_amd/build_ext.py [--jobs N]
 
 Every csrc/*.hip and csrc/*.cpp file is compiled with hipcc to an object under _build/ and linked into
-nanovllm_amd/libsd_attn.so. Packed-fp32 instruction selection is switched off for the device code.
+nanovllm_amd/libsd_attn.so. Packed-fp32 instruction selection is switched off for the device code, and MFMA
+results are selected into VGPRs.
 """
 import argparse
 import concurrent.futures
@@ -18,7 +19,11 @@ BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "nanovllm_amd", "libsd_attn.so")
 ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", f"-I{os.path.join(HERE, '..', 'include')}"]
-DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# MFMA results in VGPRs (-amdgpu-mfma-vgpr-form): kernels that need more than 256 registers a wave then keep
+# their accumulators where the VALU reads them and give the AGPRs what only MFMAs read, instead of moving
+# values between the two files every iteration (the compiler's default AGPR form).
+DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
 
 def hipcc() -> str:

@@ -576,7 +576,9 @@ __device__ __forceinline__ int rotated_head(const Params& p, int y, int z) {
 }
 
 template <int RT, bool kVarlen, bool kPaged, int kWaves>
-__global__ __launch_bounds__(kWaves * kWave, RT <= 2 ? 2 : 1) void attn_fwd(Params p) {
+// Two waves per SIMD (at most 256 registers a wave) up to three row tiles, whatever the workgroup size: the
+// second argument is the minimum waves per SIMD. Four row tiles need more registers and run one wave a SIMD.
+__global__ __launch_bounds__(kWaves * kWave, RT <= 3 ? 2 : 1) void attn_fwd(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes_rt(kWaves, RT)];
   const int h = rotated_head(p, blockIdx.y, blockIdx.z);
   if constexpr (kVarlen) {
