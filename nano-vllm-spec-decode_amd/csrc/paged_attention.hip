@@ -575,9 +575,9 @@ __device__ __forceinline__ int rotated_head(const Params& p, int y, int z) {
   return (int)((y + linear / p.wave_slots) % p.Hkv);
 }
 
-template <int RT, bool kVarlen, bool kPaged, int kWaves>
 // Two waves per SIMD (at most 256 registers a wave) up to three row tiles, whatever the workgroup size: the
 // second argument is the minimum waves per SIMD. Four row tiles need more registers and run one wave a SIMD.
+template <int RT, bool kVarlen, bool kPaged, int kWaves>
 __global__ __launch_bounds__(kWaves * kWave, RT <= 3 ? 2 : 1) void attn_fwd(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes_rt(kWaves, RT)];
   const int h = rotated_head(p, blockIdx.y, blockIdx.z);
