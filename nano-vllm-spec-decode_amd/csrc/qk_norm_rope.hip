@@ -1,9 +1,10 @@
 // Fused q/k RMSNorm + rotary embedding + paged KV store: the per-token work between the qkv projection
 // and attention (nanovllm/models/qwen3.py:83-97, then the store of nanovllm/layers/attention.py:33-40).
 //
-// One 8-lane group per (token, head) of the qkv row, heads in row order (q heads, then k, then v), so
-// consecutive groups read consecutive 256-byte head rows. Lane c holds elements 8c..8c+7 of each half of
-// the head (the halves the neox rotation pairs): two 16-byte loads.
+// One 8-lane group per (token, head) of the qkv row; a token's heads fill one workgroup (blockIdx.x = token,
+// 48 heads x 8 lanes = 384 threads for Qwen3-8B), in row order (q heads, then k, then v), so consecutive
+// groups read consecutive 256-byte head rows and the token's position and slot are scalar loads. Lane c
+// holds elements 8c..8c+7 of each half of the head (the halves the neox rotation pairs): two 16-byte loads.
 //   q / k heads: fp32 sum of squares over the head (8-lane butterfly), x * (1 / sqrt(mean + eps)) rounded
 //                to bf16, times the bf16 weight rounded to bf16 (skipped for models without q/k norm),
 //                then the rotation by the fp32 cos / sin row of the token's position, rounded to bf16.
@@ -13,6 +14,8 @@
 // no fused multiply-adds), so its only difference from them is the order of the 128-term sum of squares.
 // A position outside [0, max_position) uses NaN for cos and sin: that token's q / k come out NaN instead
 // of reading outside the table.
+#include <algorithm>
+
 #include "sd_common.h"
 #include "../../include/sd_attn.h"
 
@@ -22,7 +25,6 @@ namespace {
 constexpr int kHeadDim = 128;
 constexpr int kHalf = kHeadDim / 2;
 constexpr int kLanesPerHead = 8;  // 8 lanes x (8 + 8) elements = one head
-constexpr int kGroupsPerBlock = 256 / kLanesPerHead;
 
 struct NormRopeArgs {
   const uint16_t* q;
@@ -72,14 +74,17 @@ __device__ __forceinline__ void scale_weight(float* x, float r, const uint4& wu)
   for (int i = 0; i < 8; ++i) x[i] = to_bf16(to_bf16(x[i] * r) * w[i]);
 }
 
-__global__ __launch_bounds__(256) void qk_norm_rope_store(NormRopeArgs a) {
+__global__ __launch_bounds__(1024) void qk_norm_rope_store(NormRopeArgs a) {
 #pragma clang fp contract(off)
   const int Htot = a.Hq + a.Hkv + a.Hv;
-  const int64_t g = (int64_t)blockIdx.x * kGroupsPerBlock + threadIdx.x / kLanesPerHead;
+  // One token per workgroup row (blockIdx.x): its position and slot are workgroup-uniform (scalar loads,
+  // issued first so that the cos / sin row address is known early).
+  const int64_t t = blockIdx.x;
+  const int64_t pos = a.positions[t];
+  const int64_t slot_raw = a.k_cache != nullptr ? (int64_t)a.slots[t] : -1;
+  const int h = (int)((blockIdx.y * blockDim.x + threadIdx.x) / kLanesPerHead);
   const int c = threadIdx.x % kLanesPerHead;
-  if (g >= (int64_t)a.num_tokens * Htot) return;
-  const int64_t t = g / Htot;
-  const int h = (int)(g - t * Htot);
+  if (h >= Htot) return;
   const int kind = h < a.Hq ? 0 : (h < a.Hq + a.Hkv ? 1 : 2);  // q, k, v
   const int hh = kind == 0 ? h : (kind == 1 ? h - a.Hq : h - a.Hq - a.Hkv);
   const uint16_t* src = (kind == 0 ? a.q + t * a.q_stride : kind == 1 ? a.k + t * a.k_stride : a.v + t * a.v_stride) +
@@ -87,8 +92,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store(NormRopeArgs a) {
   const uint4 u1 = *(const uint4*)src;
   const uint4 u2 = *(const uint4*)(src + kHalf);
   int64_t slot = -1;
-  if (a.k_cache != nullptr && kind != 0) {
-    slot = a.slots[t];
+  if (kind != 0) {
+    slot = slot_raw;
     if (slot >= a.num_slots) slot = -1;
   }
   const int64_t cache_off = slot * ((int64_t)a.Hkv * kHeadDim) + (int64_t)hh * kHeadDim + c * 8;
@@ -99,7 +104,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store(NormRopeArgs a) {
     }
     return;
   }
-  const int64_t pos = a.positions[t];
   const bool pos_ok = pos >= 0 && pos < a.max_position;
   const float* cs = a.cos_sin + (pos_ok ? pos : 0) * kHeadDim + c * 8;
   const float4 c0 = *(const float4*)cs, c1 = *(const float4*)(cs + 4);
@@ -220,9 +224,12 @@ extern "C" int sd_qk_norm_rope_store(const void* q, int64_t q_row_stride, const 
   a.Hq = num_heads;
   a.Hkv = num_kv_heads;
   a.Hv = store ? num_kv_heads : 0;
-  const int64_t groups = (int64_t)num_tokens * (num_heads + num_kv_heads + a.Hv);
-  const int64_t blocks = (groups + kGroupsPerBlock - 1) / kGroupsPerBlock;
-  if (blocks > 0x7fffffff) return fail(kUnsupported, "%s: too many tokens (%d)", who, num_tokens);
-  hipLaunchKernelGGL(qk_norm_rope_store, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, a);
+  // A token's heads in one workgroup row: 8 lanes a head, up to 1024 threads a workgroup.
+  const int lanes = (num_heads + num_kv_heads + a.Hv) * kLanesPerHead;
+  const int threads = std::min(1024, (lanes + 63) / 64 * 64);
+  const int rows = (lanes + threads - 1) / threads;
+  if (rows > 65535) return fail(kUnsupported, "%s: too many heads (%d)", who, num_heads + num_kv_heads);
+  hipLaunchKernelGGL(qk_norm_rope_store, dim3((uint32_t)num_tokens, (uint32_t)rows), dim3(threads), 0,
+                     (hipStream_t)stream, a);
   return check_launch(who);
 }
