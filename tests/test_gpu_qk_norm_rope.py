@@ -101,7 +101,10 @@ def _check_caches(res, slots, Hkv):
 
 
 # (28, 4): 36 heads per token, so the 8-lane groups of one wave mix q, k and v heads of two tokens.
-@pytest.mark.parametrize("N,Hq,Hkv", [(1, 32, 8), (7, 32, 8), (64, 32, 8), (2048, 32, 8), (20, 16, 8), (33, 28, 4)])
+# (5, 128, 16) and (3, 120, 8): more than 1024 lanes a token (160 and 136 heads with v), so a token's heads
+# span two workgroups
+@pytest.mark.parametrize("N,Hq,Hkv", [(1, 32, 8), (7, 32, 8), (64, 32, 8), (2048, 32, 8), (20, 16, 8), (33, 28, 4),
+                                     (5, 128, 16), (3, 120, 8)])
 def test_norm_rope_store_vs_oracle(device, N, Hq, Hkv):
     print(f"case N={N} Hq={Hq} Hkv={Hkv}", flush=True)
     c = _case(device, N, Hq, Hkv, seed=N + Hq)
