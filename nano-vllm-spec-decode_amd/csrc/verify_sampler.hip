@@ -34,7 +34,7 @@
 namespace sd {
 namespace {
 
-constexpr int kSpans = 8;         // most spans per row (workgroups per row)
+constexpr int kSpans = 6;         // most spans per row (workgroups per row; 6 measured best of 4 / 6 / 8 / 12 / 16)
 constexpr int kPipeU = 2;         // verify_resample: 4-entry groups a lane loads per pipeline stage
 constexpr int kThreads = 256;
 
