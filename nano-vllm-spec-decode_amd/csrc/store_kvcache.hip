@@ -2,8 +2,8 @@
 //
 // One wave64 per token row. A row is num_kv_heads*head_dim bf16 elements (2 KiB for Qwen3-8B), copied
 // with 16-byte vector loads/stores: each lane moves 2 x 16 B of K and 2 x 16 B of V, all loads issued
-// before the stores. A negative slot (-1 = graph padding) returns before touching memory, so padded
-// rows of a captured graph cost one scalar load.
+// before the stores (the first ones together with the slot's load). A negative slot (-1 = graph padding)
+// stores nothing.
 #include "sd_common.h"
 #include "../../include/sd_attn.h"
 
@@ -23,12 +23,35 @@ __global__ __launch_bounds__(256) void store_kvcache_vec(const uint4* __restrict
   const int64_t idx = (int64_t)blockIdx.x * kRowsPerBlock + wave;
   if (idx >= num_tokens) return;
   const int64_t slot = slots[idx];
-  if (slot < 0 || slot >= num_slots) return;
   const uint4* ksrc = key + idx * key_stride;
   const uint4* vsrc = value + idx * value_stride;
+  // The first step's loads go out with the slot's (the source row exists whatever the slot), so the row's
+  // latency is one memory round trip, not two.
+  int i = lane;
+  const bool two = i + kWave < row_vecs, one = i < row_vecs;
+  uint4 k0{}, k1{}, v0{}, v1{};
+  if (two) {
+    k0 = ksrc[i];
+    k1 = ksrc[i + kWave];
+    v0 = vsrc[i];
+    v1 = vsrc[i + kWave];
+  } else if (one) {
+    k0 = ksrc[i];
+    v0 = vsrc[i];
+  }
+  if (slot < 0 || slot >= num_slots) return;
   uint4* kdst = k_cache + slot * row_vecs;
   uint4* vdst = v_cache + slot * row_vecs;
-  int i = lane;
+  if (two) {
+    kdst[i] = k0;
+    kdst[i + kWave] = k1;
+    vdst[i] = v0;
+    vdst[i + kWave] = v1;
+  } else if (one) {
+    kdst[i] = k0;
+    vdst[i] = v0;
+  }
+  i += 2 * kWave;
   // Two vectors of each tensor per lane per step keeps four 16-B loads in flight before the stores.
   for (; i + kWave < row_vecs; i += 2 * kWave) {
     uint4 k0 = ksrc[i], k1 = ksrc[i + kWave];
