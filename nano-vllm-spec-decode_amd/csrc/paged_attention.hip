@@ -891,25 +891,27 @@ template <bool kVarlen>
 __global__ __launch_bounds__(256) void attn_combine(Params p) {
   const int item = blockIdx.x;
   const int h = blockIdx.y;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  // One row per wave, four rows per workgroup along z: every row's loads are in flight at once, and they
+  // go out before the item's description arrives (row < rows_alloc, so they stay inside the partials; the
+  // rows past the item's are not used).
+  const int row = blockIdx.z * 4 + wave;
+  const int64_t base0 = (((int64_t)item * p.Hkv + h) * kResidues) * p.rows_alloc + row;
+  float ms[kResidues], ls[kResidues];
+  float2 os[kResidues];
+#pragma unroll
+  for (int r = 0; r < kResidues; ++r) {
+    const int64_t b = base0 + (int64_t)r * p.rows_alloc;
+    const float2 mlv = *(const float2*)(p.part_ml + b * 2);
+    ms[r] = mlv.x;
+    ls[r] = mlv.y;
+    os[r] = *(const float2*)(p.part_o + b * kD + 2 * lane);
+  }
   const Item it = describe<kVarlen>(p, item);
   if (!it.valid) return;
   const int rows = it.np * p.g;
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  // One row per wave, four rows per workgroup along z: every row's loads are in flight at once.
-  const int row = blockIdx.z * 4 + wave;
   if (row < rows) {
-    const int64_t base0 = (((int64_t)item * p.Hkv + h) * kResidues) * p.rows_alloc + row;
-    float ms[kResidues], ls[kResidues];
-    float2 os[kResidues];
-#pragma unroll
-    for (int r = 0; r < kResidues; ++r) {
-      const int64_t b = base0 + (int64_t)r * p.rows_alloc;
-      const float2 mlv = *(const float2*)(p.part_ml + b * 2);
-      ms[r] = mlv.x;
-      ls[r] = mlv.y;
-      os[r] = *(const float2*)(p.part_o + b * kD + 2 * lane);
-    }
     float M = -INFINITY;
 #pragma unroll
     for (int r = 0; r < kResidues; ++r) M = fmaxf(M, ms[r]);
