@@ -147,7 +147,7 @@ def bench_verify_uniform(dev, B=64, k=4, lo=1024, hi=8192, W=33):
 
 
 def bench_verify_sweep(dev, ctx_len=4096, W=33):
-    """The batch / guess-count points of the verify workload at ctx 4096: B in {1, 16, 64}, k in {1, 4, 8},
+    """The batch / guess-count points of the verify workload at ctx 4096: B in {1, 16, 64}, k in {1, 2, 4, 8},
     through Attention.forward's path (planned order), graph-timed over calls that each read the next of
     enough cache copies to exceed the 256 MB last-level cache."""
     import types
@@ -161,7 +161,7 @@ def bench_verify_sweep(dev, ctx_len=4096, W=33):
         kc, vc, tables = paged_cache(dev, ctx, HKV, D, W=W, seed=0)
         copies = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(max(1, 300 // (17 * B)))]
         lens = torch.tensor(ctx, dtype=torch.int32, device=dev)
-        for k in (1, 4, 8):
+        for k in (1, 2, 4, 8):
             n = k + 1
             q = queries(dev, B * n, HQ, D, seed=1).view(B, n, HQ, D)
             out = torch.empty(B * n, HQ, D, dtype=torch.bfloat16, device=dev)
