@@ -206,43 +206,50 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   const int grp = lane / 16;  // 16-lane group: which 8 k-elements / 4 accumulator rows
   int32_t* blk_ids = (int32_t*)(lds + kStageBytes + ml_bytes(kWaves));
 
-  // Decode items know their sequence without a memory read: start the block-table row loads (the whole
-  // row, ids are range-checked before use) before the context length arrives, so the prologue costs one
-  // memory round trip instead of two.
+  // The block-table row loads (the whole row, ids are range-checked before use) go out before the item's
+  // lengths arrive: a decode item knows its sequence without a memory read, a varlen item from the first
+  // word of its work-list entry (written by the plan, always a sequence of the call).
   constexpr int kBlkPerThread = (kMaxBlocks + kWaves * kWave - 1) / (kWaves * kWave);
   int32_t blk_pre[kBlkPerThread];
   const int nblk_row = min(p.table_width, kMaxBlocks);
-  if (kPaged && !kVarlen) {
-    int seq = p.seq_order ? p.seq_order[item / p.groups_per_seq] : item / p.groups_per_seq;
-    if (seq < 0 || (int64_t)seq * p.n >= p.total_q) seq = 0;  // describe() drops such an item
+  // This wave's first tile (tile `residue`) lies in table entry first_bi; its id is read with the row, as
+  // a scalar load, so that the tile's K and V loads can go out before the row reaches LDS.
+  const int first_bi = kPaged ? residue * kTile / p.block_size : 0;
+  int32_t first_blk = -1;
+  if (kPaged) {
+    int seq = 0;
+    bool listed = true;
+    if (kVarlen) {
+      listed = item < *p.work_count;
+      if (listed) seq = p.work[2 * item];
+    } else {
+      seq = p.seq_order ? p.seq_order[item / p.groups_per_seq] : item / p.groups_per_seq;
+      if (seq < 0 || (int64_t)seq * p.n >= p.total_q) seq = 0;  // describe() drops such an item
+    }
+    // Every thread loads (an index past the row reads its last id, then replaced by -1): no divergent
+    // loads, so the waits before the LDS stores below count only these loads.
 #pragma unroll
     for (int i = 0; i < kBlkPerThread; ++i) {
       const int b = tid + i * kWaves * kWave;
-      blk_pre[i] = b < nblk_row ? p.block_tables[(int64_t)seq * p.table_width + b] : -1;
+      const int32_t id = p.block_tables[(int64_t)seq * p.table_width + min(b, nblk_row - 1)];
+      blk_pre[i] = listed && b < nblk_row ? id : -1;
     }
+    if (listed) first_blk = p.block_tables[(int64_t)seq * p.table_width + min(first_bi, nblk_row - 1)];
   }
   const Item it = describe<kVarlen>(p, item);
-  if (!it.valid) return;
+  if (!it.valid) {
+    // The ids are read on this path too, so that the compiler keeps their loads ahead of the length
+    // checks instead of sinking them behind describe()'s round trips.
+    if constexpr (kPaged) {
+#pragma unroll
+      for (int i = 0; i < kBlkPerThread; ++i) asm volatile("" : : "v"(blk_pre[i]));
+      asm volatile("" : : "s"(first_blk));
+    }
+    return;
+  }
   const int rows = it.np * p.g;
   const int kmax = it.kmax;
   const int end_tile = (kmax + kTile - 1) / kTile;
-
-  // The item's block ids in LDS.
-  if (kPaged) {
-    if (kVarlen) {
-#pragma unroll
-      for (int i = 0; i < kBlkPerThread; ++i) {
-        const int b = tid + i * kWaves * kWave;
-        blk_pre[i] = b < nblk_row ? p.block_tables[(int64_t)it.seq * p.table_width + b] : -1;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kBlkPerThread; ++i) {
-      const int b = tid + i * kWaves * kWave;
-      if (b < nblk_row) blk_ids[b] = blk_pre[i];
-    }
-    __syncthreads();
-  }
 
   // Per-row visible-key limit (bottom-right causal: query i sees Lk - Lq + i + 1 keys) and the Q operand
   // (B of S^T): lane holds row 16*rt + r16, d = 32*ks + 8*grp + e.
@@ -461,11 +468,24 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   u32x4 vstage[8];
   int j = residue;
   bool cur_ok = true;
-  if (j < end_tile) {
-    const TileSrc ts = tile_src(j, __builtin_amdgcn_readfirstlane(tile_blk(j)));
-    load_v(ts, vstage);
-    load_k(ts, kreg);
+  {
+    // The first tile from first_blk. Paged, a wave without tiles loads tile 0 of block 0 and never uses
+    // it: loads on every path keep the waits before the LDS stores below exact.
+    const bool has_tile = j < end_tile;
+    const int blk0 = kPaged && has_tile && first_bi < nblk_row ? first_blk : -1;
+    const TileSrc ts = tile_src(has_tile ? j : 0, __builtin_amdgcn_readfirstlane(blk0));
+    if (kPaged || has_tile) {
+      load_v(ts, vstage);
+      load_k(ts, kreg);
+    }
     cur_ok = ts.ok;
+  }
+  // The item's block ids in LDS for the later tiles (all kMaxBlocks entries, -1 past the row).
+  if (kPaged) {
+    static_assert(kBlkPerThread * kWaves * kWave == kMaxBlocks, "one id per thread and step");
+#pragma unroll
+    for (int i = 0; i < kBlkPerThread; ++i) blk_ids[tid + i * kWaves * kWave] = blk_pre[i];
+    __syncthreads();
   }
   while (j + kResidues < end_tile) {
     const int blk_next = tile_blk(j + kResidues);
