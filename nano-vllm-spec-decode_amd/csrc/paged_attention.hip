@@ -1317,7 +1317,10 @@ int decode_run(const char* who, bool planned, const void* q, int64_t q_token_str
   launch_fwd<false, true>(RT, waves, dim3(1, num_kv_heads, (unsigned)items), s, p);
   if ((rc = check_launch(who))) return rc;
   if (partials) {
-    hipLaunchKernelGGL((attn_combine<false>), dim3((unsigned)items, num_kv_heads, (unsigned)(p.rows_alloc / 4)),
+    // Four rows a workgroup over the rows a query group can hold (P positions x g heads), not the row tiles'
+    // padding: B=16, k=4 merges 20 of 32 rows.
+    const int merge_rows = std::min(P * g, p.rows_alloc);
+    hipLaunchKernelGGL((attn_combine<false>), dim3((unsigned)items, num_kv_heads, (unsigned)((merge_rows + 3) / 4)),
                        dim3(256), 0, s, p);
     if ((rc = check_launch(who))) return rc;
   }
