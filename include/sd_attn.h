@@ -205,7 +205,9 @@ int sd_verify_drafts(const void* logits, int32_t logits_dtype, int64_t logits_ro
  * GEMM's epilogue takes each row's first argmax. With temperatures, logits_out ([S*(K+1), vocab] bf16, row
  * stride >= vocab) is required and the sampled rows are decided by sd_verify_drafts's passes over it. The
  * other arguments and the outputs are sd_verify_drafts's. No counterpart in the reference for the packing (the
- * reference's F.linear reads the weight as stored).
+ * reference's F.linear reads the weight as stored). The workspace size depends on the CU count of the current
+ * device (the GEMM's last round of workgroups may be split along hidden_dim, its fp32 sums kept there): size it
+ * with that device current and call on a stream of the same device.
  */
 size_t sd_lm_head_packed_weight_size(int32_t vocab, int32_t hidden_dim);
 int sd_lm_head_pack_weight(const void* weight, int32_t vocab, int32_t hidden_dim, void* packed_weight, void* stream);

@@ -61,7 +61,14 @@ struct Args {
   int64_t logits_stride;
   int32_t logits_vec;       // rows 8-byte aligned: 4 entries per store
   TileBest* best;           // [M][tiles]
-  int32_t tiles;            // gridDim.x
+  int32_t tiles;            // vocabulary tiles of kN rows
+  // Tiles full.. (the last, partial round of workgroups) are cut into `splits` ranges of H each, one
+  // workgroup per range, so that the last round fills the GPU; such a workgroup writes its fp32 sums to
+  // `part` ([tile - full][split][8 waves][2][MB][16][64 lanes]) and lm_head_fixup adds the ranges in order
+  // and runs the epilogue. splits = 1: every tile whole (full = tiles). Only with one row of workgroups.
+  int32_t full;
+  int32_t splits;
+  float* part;
 };
 
 // One thread per 16 bytes of the packed weight.
@@ -112,6 +119,70 @@ __device__ __forceinline__ void wait_vm() {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// Epilogue, per 32-token-row block of a tile. A lane holds 16 vocabulary entries of one token row for each of
+// its two 32-row vocabulary blocks (the other 16 in lane l ^ 32): it rounds them to bf16, stores them if the
+// logits are asked for, and takes the first argmax (index order) of its entries and its lane pair's. Returns
+// it in every lane; token row m of the call (no store, the argmax still taken, for m >= M).
+__device__ __forceinline__ TileBest block_best(const Args& a, const f32x16 (&acc)[2], int n_wave, int m) {
+  const int half = (threadIdx.x % kWave) / 32;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int nf = n_wave + 32 * nb + 8 * g + 4 * half;  // first of 4 consecutive entries
+      float v[4];
+      uint16_t bits[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bits[e] = f32_to_bf16_bits(acc[nb][4 * g + e]);
+        v[e] = bf16_bits_to_f32(bits[e]);
+      }
+      if (a.logits && m < a.M) {
+        uint16_t* dst = a.logits + (int64_t)m * a.logits_stride + nf;
+        if (nf + 3 < a.V && a.logits_vec) {
+          *(uint2*)dst = make_uint2((uint32_t)bits[0] | ((uint32_t)bits[1] << 16),
+                                    (uint32_t)bits[2] | ((uint32_t)bits[3] << 16));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (nf + e < a.V) dst[e] = bits[e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (nf + e < a.V && bv == bv && !(v[e] <= bv)) {  // index order within the lane: strictly larger
+          bv = v[e];
+          bi = nf + e;
+        }
+    }
+  }
+  const float ov = __shfl_xor(bv, 32);
+  const int oi = __shfl_xor(bi, 32);
+  if (better(ov, oi, bv, bi)) {
+    bv = ov;
+    bi = oi;
+  }
+  return TileBest{bv, bi};
+}
+
+// The four vocabulary waves' candidates of `rows` token rows (red[row][wave], in LDS, after a barrier), reduced
+// in wave order into best[m][tile] by threads 0.. of the workgroup.
+__device__ __forceinline__ void reduce_best(const Args& a, const TileBest* red, int rows, int m0, int tile) {
+  for (int mr = threadIdx.x; mr < rows; mr += blockDim.x) {
+    const int m = m0 + mr;
+    if (m >= a.M) continue;
+    TileBest b = red[mr * 4];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const TileBest o = red[mr * 4 + w];
+      if (better(o.val, o.idx, b.val, b.idx)) b = o;
+    }
+    a.best[(int64_t)m * a.tiles + tile] = b;
+  }
+}
+
 template <int MB>
 __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
   static_assert(MB >= 1 && MB <= kMaxMB, "token blocks per wave");
@@ -121,9 +192,17 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
   const int lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int wn = wave % 4, wm = wave / 4;
-  const int n0 = blockIdx.x * kN;
+  // This workgroup's tile and range of H stages (the whole of H, or one range of a split tile).
+  const int S = a.H / kK;
+  int tile = blockIdx.x, split = -1, s_begin = 0, nstages = S;
+  if ((int)blockIdx.x >= a.full) {
+    const int j = blockIdx.x - a.full;
+    tile = a.full + j / a.splits;
+    split = j % a.splits;
+    s_begin = split * S / a.splits;
+    nstages = (split + 1) * S / a.splits - s_begin;
+  }
   const int m0 = blockIdx.y * kRows;
-  const int H = a.H;
 
   // Stage loads straight into LDS (global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's LDS
   // base + 16 l, i.e. row l / 4, physical chunk l % 4 of a 16-row group; so the lane fetches the logical chunk
@@ -134,7 +213,6 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
   const bool wloader = wave < 4;
   constexpr int kLoads = MB > 4 ? MB : 4;          // instructions per stage of the busiest loader
   const int nloads = wloader ? 4 : MB;
-  const int S = H / kK;
   uint32_t loff[kLoads], goff[kLoads];             // LDS offset; element offset within the stage tile
 #pragma unroll
   for (int i = 0; i < kLoads; ++i) {
@@ -142,14 +220,13 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
     goff[i] = 16 * g * 32 + lane_off;
     loff[i] = (wloader ? 0 : kWBytes) + 16 * g * kRowBytes;
   }
-  // Each workgroup starts its walk over H at its own stage (a rotation: the fp32 sums of a tile run in that
-  // order), so that the workgroups do not all read the same hidden stage at once.
-  const int nstages = S;
+  // Each workgroup starts its walk over its stages at its own stage (a rotation: the fp32 sums of a tile or
+  // range run in that order), so that the workgroups do not all read the same hidden stage at once.
   const int rot = (int)((blockIdx.x * 37u) % (unsigned)nstages);
   auto issue = [&](int st) {
     uint8_t* ring = lds + (st % kRing) * kStageBytes;
-    const int ks = (st + rot) % nstages;
-    const uint16_t* base = wloader ? a.wp + ((int64_t)blockIdx.x * S + ks) * (kN * kK)
+    const int ks = s_begin + (st + rot) % nstages;
+    const uint16_t* base = wloader ? a.wp + ((int64_t)tile * S + ks) * (kN * kK)
                                    : a.hp + ((int64_t)ks * a.Mpad + m0) * kK;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i)
@@ -214,67 +291,67 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
     mfmas(a1, b1);
   }
 
-  // Epilogue: per token row, the first argmax over this lane's 32 entries (index order), its lane pair and
-  // the four vocabulary waves.
+  if (split >= 0) {
+    // ---- one range of a split tile: the fp32 sums out, lm_head_fixup finishes the tile ----
+    float* dst = a.part + ((int64_t)(blockIdx.x - a.full) * kWaves + wave) * (2 * MB * 16 * kWave) + lane;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[((nb * MB + mb) * 16 + r) * kWave] = acc[nb][mb][r];
+    return;
+  }
+  // ---- epilogue: per token row, the first argmax over the workgroup's 256 vocabulary rows ----
   __syncthreads();  // every wave's last stage read: the ring is free for the reduction
   TileBest* red = (TileBest*)lds;  // [kRows][4]
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int mr = MB * 32 * wm + 32 * mb + col;  // token row within the workgroup
-    const int m = m0 + mr;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int nf = n0 + 64 * wn + 32 * nb + 8 * g + 4 * half;  // first of 4 consecutive entries
-        float v[4];
-        uint16_t bits[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          bits[e] = f32_to_bf16_bits(acc[nb][mb][4 * g + e]);
-          v[e] = bf16_bits_to_f32(bits[e]);
-        }
-        if (a.logits && m < a.M) {
-          uint16_t* dst = a.logits + (int64_t)m * a.logits_stride + nf;
-          if (nf + 3 < a.V && a.logits_vec) {
-            *(uint2*)dst = make_uint2((uint32_t)bits[0] | ((uint32_t)bits[1] << 16),
-                                      (uint32_t)bits[2] | ((uint32_t)bits[3] << 16));
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (nf + e < a.V) dst[e] = bits[e];
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (nf + e < a.V && bv == bv && !(v[e] <= bv)) {  // index order within the lane: strictly larger
-            bv = v[e];
-            bi = nf + e;
-          }
-      }
-    }
-    const float ov = __shfl_xor(bv, 32);
-    const int oi = __shfl_xor(bi, 32);
-    if (better(ov, oi, bv, bi)) {
-      bv = ov;
-      bi = oi;
-    }
-    if (half == 0) red[mr * 4 + wn] = TileBest{bv, bi};
+    const f32x16 blk[2] = {acc[0][mb], acc[1][mb]};
+    const TileBest b = block_best(a, blk, tile * kN + 64 * wn, m0 + mr);
+    if (half == 0) red[mr * 4 + wn] = b;
   }
   __syncthreads();
-  for (int mr = tid; mr < kRows; mr += kThreads) {
-    const int m = m0 + mr;
-    if (m >= a.M) continue;
-    TileBest b = red[mr * 4];
+  reduce_best(a, red, kRows, m0, tile);
+}
+
+// The tiles split along H: one 4-wave workgroup per (split tile, 32-token-row block) adds the ranges' sums in
+// range order and finishes the block as lm_head_gemm's epilogue does. Wave w takes the vocabulary rows of the
+// GEMM's wave w of the block's token half: 64 w .. 64 w + 63.
+template <int MB>
+__global__ __launch_bounds__(256) void lm_head_fixup(Args a) {
+  __shared__ TileBest red[32 * 4];
+  const int lane = threadIdx.x % kWave;
+  const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wm = blockIdx.y / MB, mb = blockIdx.y % MB;
+  const int tile = a.full + blockIdx.x;
+  constexpr int kPerWave = 2 * MB * 16 * kWave;
+  const float* src = a.part + ((int64_t)blockIdx.x * a.splits * kWaves + 4 * wm + wn) * kPerWave + mb * 16 * kWave +
+                     lane;
+  f32x16 acc[2];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) {
-      const TileBest o = red[mr * 4 + w];
-      if (better(o.val, o.idx, b.val, b.idx)) b = o;
-    }
-    a.best[(int64_t)m * a.tiles + blockIdx.x] = b;
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[nb][r] = src[(nb * MB * 16 + r) * kWave];
+  for (int sp = 1; sp < a.splits; ++sp) {
+    const float* p = src + (int64_t)sp * kWaves * kPerWave;
+    float t[2][16];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) t[nb][r] = p[(nb * MB * 16 + r) * kWave];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[nb][r] += t[nb][r];
   }
+  const int col = lane % 32;
+  const int mr = MB * 32 * wm + 32 * mb + col;
+  const TileBest b = block_best(a, acc, tile * kN + 64 * wn, mr);
+  if (lane < 32) red[col * 4 + wn] = b;
+  __syncthreads();
+  reduce_best(a, red, 32, MB * 32 * wm + 32 * mb, tile);
 }
 
 }  // namespace lmhead

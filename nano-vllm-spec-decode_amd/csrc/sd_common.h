@@ -98,4 +98,19 @@ __device__ __forceinline__ bf16x8 ds_read_b128(uint32_t addr) {
   return r;
 }
 
+// CUs of the device that runs `stream` (the null stream: the current device's), queried once per device.
+// Host code only.
+inline int cu_count(hipStream_t stream) {
+  static int cached[64];  // per device; 0 until first queried (a racing second query stores the same value)
+  hipDevice_t dev = 0;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess && hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev < 0 || dev >= 64) return 256;
+  int cus = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  if (!cus) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    __atomic_store_n(&cached[dev], cus, __ATOMIC_RELAXED);
+  }
+  return cus;
+}
+
 }  // namespace sd

@@ -910,32 +910,63 @@ int64_t lm_head_mpad(int64_t M) {
   return (M + 64 * MB - 1) / (64 * MB) * (64 * MB);
 }
 
-struct LmLayout {
-  size_t best, stats, info, hp, total;
+// The GEMM runs one workgroup per CU. When the grid's last round holds at most half as many tiles as there are
+// CUs, those tiles are split along H into min(4, CUs / tail, H / 32) ranges (a single row of workgroups only).
+struct LmSplit {
+  int full, splits;
 };
-LmLayout lm_layout(int S, int K, int V, int H) {
+LmSplit lm_head_split(int64_t M, int V, int H, int cus) {
+  const int tiles = (V + lmhead::kN - 1) / lmhead::kN;
+  const int MB = lm_head_mb((int)std::min<int64_t>(M, 0x7fffffff));
+  LmSplit r{tiles, 1};
+  if (lm_head_mpad(M) != 64 * MB || cus <= 0) return r;
+  const int tail = tiles - (tiles - 1) / cus * cus;  // tiles of the last round, 1..cus
+  if (2 * tail > cus) return r;
+  const int splits = std::min({4, cus / tail, H / lmhead::kK});
+  if (splits < 2) return r;
+  r.full = tiles - tail;
+  r.splits = splits;
+  return r;
+}
+
+struct LmLayout {
+  size_t best, stats, info, hp, part, total;
+};
+LmLayout lm_layout(int S, int K, int V, int H, int cus) {
   const int64_t M = (int64_t)S * (K + 1);
   const int tiles = (V + lmhead::kN - 1) / lmhead::kN;
+  const LmSplit sp = lm_head_split(M, V, H, cus);
+  const size_t part_bytes = sp.splits > 1 ? (size_t)(tiles - sp.full) * sp.splits * lmhead::kWaves * 2 *
+                                                 lm_head_mb((int)M) * 16 * kWave * sizeof(float)
+                                          : 0;
   LmLayout L;
   L.best = 0;
   L.stats = align256((size_t)M * tiles * sizeof(lmhead::TileBest));
   L.info = align256(L.stats + (size_t)M * sizeof(RowStat));
   L.hp = align256(L.info + (size_t)S * sizeof(SeqInfo));
-  L.total = align256(L.hp + (size_t)lm_head_mpad(M) * H * 2);
+  L.part = align256(L.hp + (size_t)lm_head_mpad(M) * H * 2);
+  L.total = align256(L.part + part_bytes);
   return L;
 }
 
+template <int MB>
+int launch_lm_head_mb(const lmhead::Args& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.full + (a.tiles - a.full) * a.splits), (unsigned)(a.Mpad / (64 * MB)));
+  hipLaunchKernelGGL(lmhead::lm_head_gemm<MB>, grid, dim3(lmhead::kThreads), 0, s, a);
+  int rc = check_launch("lm_head_gemm");
+  if (rc || a.splits == 1) return rc;
+  hipLaunchKernelGGL(lmhead::lm_head_fixup<MB>, dim3((unsigned)(a.tiles - a.full), 2 * MB), dim3(256), 0, s, a);
+  return check_launch("lm_head_fixup");
+}
+
 int launch_lm_head(const lmhead::Args& a, hipStream_t s) {
-  const int MB = lm_head_mb(a.M);
-  const dim3 grid((unsigned)a.tiles, (unsigned)(a.Mpad / (64 * MB)));
-  switch (MB) {
-    case 1: hipLaunchKernelGGL(lmhead::lm_head_gemm<1>, grid, dim3(lmhead::kThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(lmhead::lm_head_gemm<2>, grid, dim3(lmhead::kThreads), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(lmhead::lm_head_gemm<3>, grid, dim3(lmhead::kThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(lmhead::lm_head_gemm<4>, grid, dim3(lmhead::kThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL(lmhead::lm_head_gemm<5>, grid, dim3(lmhead::kThreads), 0, s, a); break;
+  switch (lm_head_mb(a.M)) {
+    case 1: return launch_lm_head_mb<1>(a, s);
+    case 2: return launch_lm_head_mb<2>(a, s);
+    case 3: return launch_lm_head_mb<3>(a, s);
+    case 4: return launch_lm_head_mb<4>(a, s);
+    default: return launch_lm_head_mb<5>(a, s);
   }
-  return check_launch("lm_head_gemm");
 }
 
 // Scratch of the allocation-free entry point: one copy per GPU (a __device__ variable lives in every device's
@@ -1058,7 +1089,7 @@ extern "C" int sd_lm_head_pack_weight(const void* weight, int32_t vocab, int32_t
 extern "C" size_t sd_lm_head_verify_workspace_size(int32_t num_seqs, int32_t num_draft_slots, int32_t vocab,
                                                    int32_t hidden_dim, int32_t has_draft_logits) {
   if (num_seqs <= 0 || num_draft_slots < 0 || vocab <= 0 || hidden_dim <= 0) return 0;
-  return std::max(lm_layout(num_seqs, num_draft_slots, vocab, hidden_dim).total,
+  return std::max(lm_layout(num_seqs, num_draft_slots, vocab, hidden_dim, cu_count(nullptr)).total,
                   verify_layout(num_seqs, num_draft_slots, vocab, has_draft_logits && num_draft_slots > 0).total);
 }
 
@@ -1091,11 +1122,13 @@ extern "C" int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, 
   if (hidden_rows < (logits_indices ? 1 : M))
     return fail(kBadArgument, "%s: hidden has %d rows (needs %s)", who, hidden_rows,
                 logits_indices ? "at least 1" : "one per token row");
-  const size_t need = sd_lm_head_verify_workspace_size(S, K, V, H, draft_logits != nullptr);
+  hipStream_t s = (hipStream_t)stream;
+  const int cus = cu_count(s);
+  const LmLayout lay = lm_layout(S, K, V, H, cus);
+  const size_t need =
+      std::max(lay.total, verify_layout(S, K, V, draft_logits != nullptr && K > 0).total);
   if (!workspace || workspace_bytes < need)
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, need);
-  const LmLayout lay = lm_layout(S, K, V, H);
-  hipStream_t s = (hipStream_t)stream;
   lmhead::Args a{};
   a.Mpad = (int32_t)lm_head_mpad(M);
   a.hp = (const uint16_t*)((uint8_t*)workspace + lay.hp);
@@ -1108,6 +1141,10 @@ extern "C" int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, 
   a.logits_vec = (uintptr_t)logits_out % 8 == 0 && logits_out_row_stride % 4 == 0;
   a.best = (lmhead::TileBest*)((uint8_t*)workspace + lay.best);
   a.tiles = (V + lmhead::kN - 1) / lmhead::kN;
+  const LmSplit split = lm_head_split(M, V, H, cus);
+  a.full = split.full;
+  a.splits = split.splits;
+  a.part = (float*)((uint8_t*)workspace + lay.part);
   const int64_t hchunks = (int64_t)(H / 32) * a.Mpad * 4;
   hipLaunchKernelGGL(lmhead::lm_head_pack_hidden, dim3((unsigned)((hchunks + 255) / 256)), dim3(256), 0, s,
                      (const uint16_t*)hidden, hidden_row_stride, hidden_rows, logits_indices, a.M, a.Mpad, H,
