@@ -96,3 +96,23 @@ def test_lm_head_verify_against_library_gemm_logits(device):
     print(f"vs F.linear: {same * 100:.3f} % identical, {int(big.sum())} entries differ by more than one bf16 unit "
           f"+ 1e-3", flush=True)
     assert same >= 0.99 and int(big.sum()) == 0
+
+
+def test_lm_head_verify_repeatable(device):
+    """Two calls at Qwen3-8B's shape give bitwise equal logits and decisions: the vocabulary tiles of the GEMM's
+    last round are computed in ranges of H whose fp32 sums are added in a fixed order."""
+    S, K, V, H = 64, 4, 151936, 4096
+    hidden, weight, _ = _inputs(device, 11, S, K, V, H)
+    head = LMHeadVerifier(weight)
+    drafts = torch.randint(0, V, (S, K), generator=torch.Generator().manual_seed(3)).to(device)
+    nd = torch.full((S,), K, dtype=torch.int64, device=device)
+    zeros = torch.zeros(S, device=device)
+    outs = []
+    for _ in range(2):
+        out = torch.empty(S * (K + 1), V, dtype=torch.bfloat16, device=device)
+        a, t = lm_head_verify(hidden, head, drafts, nd, zeros, logits_out=out)
+        outs.append((out, a.cpu(), t.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
+    # the last 82 tiles (vocabulary rows from 131072 on) meet the same bar as the others
+    _check_logits(hidden, weight[131072:], None, outs[0][0].cpu()[:, 131072:].contiguous(), [0, 100, 319])
