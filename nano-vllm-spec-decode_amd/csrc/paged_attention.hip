@@ -33,7 +33,6 @@
 #include <math.h>
 
 #include <algorithm>
-#include <atomic>
 #include <climits>
 
 #include "prefill_attention.h"
@@ -1121,20 +1120,8 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan(const int32_t* __res
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// CUs of the device that runs `stream` (the number of 8-wave workgroups it runs at once), queried once per
-// device. The null stream is the current device's.
-int wave_slots(hipStream_t stream) {
-  static std::atomic<int> cached[64];  // per device; 0 until first queried (threads may race to fill it)
-  hipDevice_t dev = 0;
-  if (hipStreamGetDevice(stream, &dev) != hipSuccess && hipGetDevice(&dev) != hipSuccess) return 256;
-  if (dev < 0 || dev >= 64) return 256;
-  int cus = cached[dev].load(std::memory_order_relaxed);
-  if (!cus) {
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev].store(cus, std::memory_order_relaxed);
-  }
-  return cus;
-}
+// The number of 8-wave workgroups the device that runs `stream` holds at once: one per CU.
+int wave_slots(hipStream_t stream) { return cu_count(stream); }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
