@@ -64,12 +64,22 @@ struct Args {
   int32_t tiles;            // vocabulary tiles of kN rows
   // Tiles full.. (the last, partial round of workgroups) are cut into `splits` ranges of H each, one
   // workgroup per range, so that the last round fills the GPU; such a workgroup writes its fp32 sums to
-  // `part` ([tile - full][split][8 waves][2][MB][16][64 lanes]) and lm_head_fixup adds the ranges in order
-  // and runs the epilogue. splits = 1: every tile whole (full = tiles). Only with one row of workgroups.
+  // `part` ([row of workgroups][tile - full][split][8 waves][2][MB][16][64 lanes]) and lm_head_fixup adds the
+  // ranges in order and runs the epilogue. splits = 1: every tile whole (full = tiles). full and splits are
+  // functions of (V, H) only and every row of workgroups uses them, so a token row's logits do not depend on
+  // how many rows the call has.
   int32_t full;
   int32_t splits;
   float* part;
 };
+
+// The fp32 sums of tile `tile`, range `split` (-1: the whole tile), run over the H stages in a rotated order
+// that starts at this stage; it depends on the tile and range only (never on the grid), so that the
+// workgroups of a call start their walks at different hidden stages.
+__device__ __forceinline__ int stage_rotation(const Args& a, int tile, int split, int nstages) {
+  const unsigned key = split < 0 ? (unsigned)tile : (unsigned)(a.full + (tile - a.full) * a.splits + split);
+  return (int)((key * 37u) % (unsigned)nstages);
+}
 
 // One thread per 16 bytes of the packed weight.
 __global__ __launch_bounds__(256) void lm_head_pack_weight(const uint16_t* __restrict__ w, int32_t V, int32_t H,
@@ -220,9 +230,7 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
     goff[i] = 16 * g * 32 + lane_off;
     loff[i] = (wloader ? 0 : kWBytes) + 16 * g * kRowBytes;
   }
-  // Each workgroup starts its walk over its stages at its own stage (a rotation: the fp32 sums of a tile or
-  // range run in that order), so that the workgroups do not all read the same hidden stage at once.
-  const int rot = (int)((blockIdx.x * 37u) % (unsigned)nstages);
+  const int rot = stage_rotation(a, tile, split, nstages);
   auto issue = [&](int st) {
     uint8_t* ring = lds + (st % kRing) * kStageBytes;
     const int ks = s_begin + (st + rot) % nstages;
@@ -293,7 +301,8 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
 
   if (split >= 0) {
     // ---- one range of a split tile: the fp32 sums out, lm_head_fixup finishes the tile ----
-    float* dst = a.part + ((int64_t)(blockIdx.x - a.full) * kWaves + wave) * (2 * MB * 16 * kWave) + lane;
+    const int64_t range = (int64_t)blockIdx.y * (a.tiles - a.full) * a.splits + (blockIdx.x - a.full);
+    float* dst = a.part + (range * kWaves + wave) * (2 * MB * 16 * kWave) + lane;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
@@ -316,9 +325,9 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
   reduce_best(a, red, kRows, m0, tile);
 }
 
-// The tiles split along H: one 4-wave workgroup per (split tile, 32-token-row block) adds the ranges' sums in
-// range order and finishes the block as lm_head_gemm's epilogue does. Wave w takes the vocabulary rows of the
-// GEMM's wave w of the block's token half: 64 w .. 64 w + 63.
+// The tiles split along H: one 4-wave workgroup per (split tile, 32-token-row block, row of GEMM workgroups)
+// adds the ranges' sums in range order and finishes the block as lm_head_gemm's epilogue does. Wave w takes
+// the vocabulary rows of the GEMM's wave w of the block's token half: 64 w .. 64 w + 63.
 template <int MB>
 __global__ __launch_bounds__(256) void lm_head_fixup(Args a) {
   __shared__ TileBest red[32 * 4];
@@ -326,9 +335,10 @@ __global__ __launch_bounds__(256) void lm_head_fixup(Args a) {
   const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int wm = blockIdx.y / MB, mb = blockIdx.y % MB;
   const int tile = a.full + blockIdx.x;
+  const int m0 = blockIdx.z * (2 * MB * 32);       // first token row of the GEMM's row of workgroups
   constexpr int kPerWave = 2 * MB * 16 * kWave;
-  const float* src = a.part + ((int64_t)blockIdx.x * a.splits * kWaves + 4 * wm + wn) * kPerWave + mb * 16 * kWave +
-                     lane;
+  const int64_t range0 = ((int64_t)blockIdx.z * (a.tiles - a.full) + blockIdx.x) * a.splits;
+  const float* src = a.part + (range0 * kWaves + 4 * wm + wn) * kPerWave + mb * 16 * kWave + lane;
   f32x16 acc[2];
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb)
@@ -348,10 +358,10 @@ __global__ __launch_bounds__(256) void lm_head_fixup(Args a) {
   }
   const int col = lane % 32;
   const int mr = MB * 32 * wm + 32 * mb + col;
-  const TileBest b = block_best(a, acc, tile * kN + 64 * wn, mr);
+  const TileBest b = block_best(a, acc, tile * kN + 64 * wn, m0 + mr);
   if (lane < 32) red[col * 4 + wn] = b;
   __syncthreads();
-  reduce_best(a, red, 32, MB * 32 * wm + 32 * mb, tile);
+  reduce_best(a, red, 32, m0 + MB * 32 * wm + 32 * mb, tile);
 }
 
 }  // namespace lmhead

@@ -910,19 +910,21 @@ int64_t lm_head_mpad(int64_t M) {
   return (M + 64 * MB - 1) / (64 * MB) * (64 * MB);
 }
 
-// The GEMM runs one workgroup per CU. When the grid's last round holds at most half as many tiles as there are
-// CUs, those tiles are split along H into min(4, CUs / tail, H / 32) ranges (a single row of workgroups only).
+// The GEMM runs one workgroup per CU. When the last round of its tiles, on a GPU of kSplitCUs CUs (MI355X's
+// count), holds at most half as many tiles as there are CUs, those tiles are split along H into
+// min(4, kSplitCUs / tail, H / 32) ranges. The choice depends on (V, H) only, never on the call's token rows
+// or on the device it runs on, and every row of workgroups applies it: a token row's fp32 sums, and so its
+// logits, are the same in every call (greedy speculative and plain decoding rely on it).
+constexpr int kSplitCUs = 256;
 struct LmSplit {
   int full, splits;
 };
-LmSplit lm_head_split(int64_t M, int V, int H, int cus) {
+LmSplit lm_head_split(int V, int H) {
   const int tiles = (V + lmhead::kN - 1) / lmhead::kN;
-  const int MB = lm_head_mb((int)std::min<int64_t>(M, 0x7fffffff));
   LmSplit r{tiles, 1};
-  if (lm_head_mpad(M) != 64 * MB || cus <= 0) return r;
-  const int tail = tiles - (tiles - 1) / cus * cus;  // tiles of the last round, 1..cus
-  if (2 * tail > cus) return r;
-  const int splits = std::min({4, cus / tail, H / lmhead::kK});
+  const int tail = tiles - (tiles - 1) / kSplitCUs * kSplitCUs;  // tiles of the last round, 1..kSplitCUs
+  if (2 * tail > kSplitCUs) return r;
+  const int splits = std::min({4, kSplitCUs / tail, H / lmhead::kK});
   if (splits < 2) return r;
   r.full = tiles - tail;
   r.splits = splits;
@@ -932,12 +934,14 @@ LmSplit lm_head_split(int64_t M, int V, int H, int cus) {
 struct LmLayout {
   size_t best, stats, info, hp, part, total;
 };
-LmLayout lm_layout(int S, int K, int V, int H, int cus) {
+LmLayout lm_layout(int S, int K, int V, int H) {
   const int64_t M = (int64_t)S * (K + 1);
   const int tiles = (V + lmhead::kN - 1) / lmhead::kN;
-  const LmSplit sp = lm_head_split(M, V, H, cus);
-  const size_t part_bytes = sp.splits > 1 ? (size_t)(tiles - sp.full) * sp.splits * lmhead::kWaves * 2 *
-                                                 lm_head_mb((int)M) * 16 * kWave * sizeof(float)
+  const LmSplit sp = lm_head_split(V, H);
+  const int MB = lm_head_mb((int)M);
+  const int64_t grid_rows = lm_head_mpad(M) / (64 * MB);
+  const size_t part_bytes = sp.splits > 1 ? (size_t)grid_rows * (tiles - sp.full) * sp.splits * lmhead::kWaves * 2 *
+                                                 MB * 16 * kWave * sizeof(float)
                                           : 0;
   LmLayout L;
   L.best = 0;
@@ -955,7 +959,8 @@ int launch_lm_head_mb(const lmhead::Args& a, hipStream_t s) {
   hipLaunchKernelGGL(lmhead::lm_head_gemm<MB>, grid, dim3(lmhead::kThreads), 0, s, a);
   int rc = check_launch("lm_head_gemm");
   if (rc || a.splits == 1) return rc;
-  hipLaunchKernelGGL(lmhead::lm_head_fixup<MB>, dim3((unsigned)(a.tiles - a.full), 2 * MB), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(lmhead::lm_head_fixup<MB>, dim3((unsigned)(a.tiles - a.full), 2 * MB, grid.y), dim3(256), 0, s,
+                     a);
   return check_launch("lm_head_fixup");
 }
 
@@ -1089,7 +1094,7 @@ extern "C" int sd_lm_head_pack_weight(const void* weight, int32_t vocab, int32_t
 extern "C" size_t sd_lm_head_verify_workspace_size(int32_t num_seqs, int32_t num_draft_slots, int32_t vocab,
                                                    int32_t hidden_dim, int32_t has_draft_logits) {
   if (num_seqs <= 0 || num_draft_slots < 0 || vocab <= 0 || hidden_dim <= 0) return 0;
-  return std::max(lm_layout(num_seqs, num_draft_slots, vocab, hidden_dim, cu_count(nullptr)).total,
+  return std::max(lm_layout(num_seqs, num_draft_slots, vocab, hidden_dim).total,
                   verify_layout(num_seqs, num_draft_slots, vocab, has_draft_logits && num_draft_slots > 0).total);
 }
 
@@ -1123,8 +1128,7 @@ extern "C" int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, 
     return fail(kBadArgument, "%s: hidden has %d rows (needs %s)", who, hidden_rows,
                 logits_indices ? "at least 1" : "one per token row");
   hipStream_t s = (hipStream_t)stream;
-  const int cus = cu_count(s);
-  const LmLayout lay = lm_layout(S, K, V, H, cus);
+  const LmLayout lay = lm_layout(S, K, V, H);
   const size_t need =
       std::max(lay.total, verify_layout(S, K, V, draft_logits != nullptr && K > 0).total);
   if (!workspace || workspace_bytes < need)
@@ -1141,7 +1145,7 @@ extern "C" int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, 
   a.logits_vec = (uintptr_t)logits_out % 8 == 0 && logits_out_row_stride % 4 == 0;
   a.best = (lmhead::TileBest*)((uint8_t*)workspace + lay.best);
   a.tiles = (V + lmhead::kN - 1) / lmhead::kN;
-  const LmSplit split = lm_head_split(M, V, H, cus);
+  const LmSplit split = lm_head_split(V, H);
   a.full = split.full;
   a.splits = split.splits;
   a.part = (float*)((uint8_t*)workspace + lay.part);

@@ -6,6 +6,12 @@ When every row is greedy the logits are never materialised: the GEMM's epilogue 
 With sampled rows the logits are written (bf16, as the library GEMM rounds them) and verified by the same passes
 as ``verify_drafts``. The weight is read in a tile layout made once per weight (``pack_weight``; LMHeadVerifier
 keeps it). Launches go on torch's current stream.
+
+A token row's logits are bitwise the same whatever the call's row count, so every consumer of greedy logits
+goes through this one GEMM: ``lm_head_verify`` (verify step, model_runner.py:481-483), ``lm_head_sample``
+(plain decode and prefill: ``compute_logits`` + ``Sampler``, model_runner.py:402,412) and ``lm_head_mixed``
+(the mixed step's verify rows and finished prefill chunks in one pass over the weight, model_runner.py:513-533).
+Greedy speculative decoding then picks the tokens plain decoding picks.
 """
 import torch
 
@@ -88,3 +94,55 @@ def lm_head_verify(hidden: torch.Tensor, head: LMHeadVerifier, draft_token_ids: 
         ws.data_ptr(), ws.numel(), _lib.stream_of(device))
     _lib.check(rc, "sd_lm_head_verify")
     return num_accepted, next_token
+
+
+def lm_head_sample(hidden: torch.Tensor, head: LMHeadVerifier, temperatures: torch.Tensor,
+                   logits_indices: torch.Tensor | None = None, exp_noise: torch.Tensor | None = None,
+                   logits_out: torch.Tensor | None = None) -> torch.Tensor:
+    """next_token [S] int64 for S rows of hidden (gathered by logits_indices when given, else its first S rows):
+    ``Sampler()(compute_logits(hidden), temperatures)`` (nanovllm/layers/sampler.py:7-16,
+    nanovllm/layers/embed_head.py:56-68) through the same GEMM as lm_head_verify, as a verify call with no
+    draft slots."""
+    S = temperatures.numel()
+    device = hidden.device
+    empty = torch.zeros(S, 0, dtype=torch.int64, device=device)
+    nd = torch.zeros(S, dtype=torch.int64, device=device)
+    return lm_head_verify(hidden, head, empty, nd, temperatures, logits_indices=logits_indices, exp_noise=exp_noise,
+                          logits_out=logits_out)[1]
+
+
+def mixed_rows(logits_indices: torch.Tensor, num_decode: int, k: int) -> torch.Tensor:
+    """The verify call's row list for a mixed step: the D(1+k) decode rows, then each finished prefill chunk's
+    row once per slot of a (1+k)-row sequence that has no drafts (only its first row decides its token)."""
+    idx = logits_indices.to(torch.int64)
+    head = idx[:num_decode * (1 + k)]
+    tail = idx[num_decode * (1 + k):]
+    return torch.cat([head, tail.repeat_interleave(1 + k)])
+
+
+def lm_head_mixed(hidden: torch.Tensor, head: LMHeadVerifier, logits_indices: torch.Tensor, num_decode: int,
+                  draft_token_ids: torch.Tensor | None, num_drafts: torch.Tensor | None,
+                  temperatures: torch.Tensor, prefill_temperatures: torch.Tensor,
+                  uniforms: torch.Tensor | None = None, exp_noise: torch.Tensor | None = None
+                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The token decisions of a mixed step (nanovllm/engine/model_runner.py:513-533) in one pass over the LM head
+    weight: (num_accepted [D], next_token [D], first_token [P]) for the D decode requests (k = the width of
+    draft_token_ids [D, k], or 0 when it is None) and the P finished prefill chunks whose rows logits_indices
+    lists after the decode rows (mixed_batch, model_runner.py:58-61). temperatures [D] and
+    prefill_temperatures [P] as the reference's; uniforms [D+P, k] / exp_noise [D+P, V] inject the noise of
+    the D decode requests, then the P chunks."""
+    device = hidden.device
+    k = 0 if draft_token_ids is None else draft_token_ids.size(1)
+    D = num_decode
+    P = logits_indices.numel() - D * (1 + k)
+    if P < 0:
+        raise ValueError("lm_head_mixed: logits_indices lists fewer than num_decode * (1 + k) rows")
+    drafts = torch.zeros(D + P, k, dtype=torch.int64, device=device)
+    nd = torch.zeros(D + P, dtype=torch.int64, device=device)
+    if k:
+        drafts[:D] = draft_token_ids
+        nd[:D] = num_drafts
+    temps = torch.cat([temperatures.float().to(device), prefill_temperatures.float().to(device)])
+    acc, nxt = lm_head_verify(hidden, head, drafts, nd, temps, logits_indices=mixed_rows(logits_indices, D, k),
+                              uniforms=uniforms, exp_noise=exp_noise)
+    return acc[:D], nxt[:D], nxt[D:]

@@ -9,7 +9,7 @@ the 256-row tile and more token rows than one workgroup holds.
 import pytest
 import torch
 
-from nanovllm_amd.layers.lm_head import LMHeadVerifier, lm_head_verify
+from nanovllm_amd.layers.lm_head import LMHeadVerifier, lm_head_mixed, lm_head_sample, lm_head_verify
 from oracle import sampler as osmp
 
 pytestmark = pytest.mark.gpu
@@ -116,3 +116,69 @@ def test_lm_head_verify_repeatable(device):
     assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
     # the last 82 tiles (vocabulary rows from 131072 on) meet the same bar as the others
     _check_logits(hidden, weight[131072:], None, outs[0][0].cpu()[:, 131072:].contiguous(), [0, 100, 319])
+
+
+def test_lm_head_logits_independent_of_row_count(device):
+    """The same hidden rows give bitwise-equal logits and argmax in calls of M = 16, 64, 320, 325 and 640 token
+    rows at Qwen3-8B's head shape (plain decode of 16 and 64 sequences, verify of 64, 65 and 128 sequences with
+    k = 4): which vocabulary tiles are split along H, and into how many ranges, follows from (V, H) alone, and
+    every row of workgroups applies it. Greedy speculative and plain decoding therefore see the same logits
+    (the reference's padding check covers GEMMs too: scripts/check_padding.py:46-52)."""
+    V, H, P = 151936, 4096, 16
+    g = torch.Generator(device=device).manual_seed(21)
+    hidden = torch.randn(700, H, device=device, generator=g).to(torch.bfloat16)
+    weight = (torch.randn(V, H, device=device, generator=g) * H ** -0.5 * 3).to(torch.bfloat16)
+    head = LMHeadVerifier(weight)
+    first = None
+    for S, K in [(16, 0), (64, 0), (64, 4), (65, 4), (128, 4)]:
+        M = S * (K + 1)
+        # the P probe rows first, then other rows in a shuffled order
+        idx = torch.cat([torch.arange(P, device=device),
+                         P + torch.randperm(700 - P, device=device, generator=g)[:M - P]])
+        out = torch.empty(M, V, dtype=torch.bfloat16, device=device)
+        zeros = torch.zeros(S, device=device)
+        _, nxt = lm_head_verify(hidden, head, torch.zeros(S, K, dtype=torch.int64, device=device),
+                                torch.zeros(S, dtype=torch.int64, device=device), zeros, logits_indices=idx,
+                                logits_out=out)
+        probe = out[:P].clone()
+        if first is None:
+            first = probe
+            # K = 0: the next tokens are the rows' first argmax
+            assert torch.equal(nxt.cpu(), probe.float().cpu().argmax(-1))
+        same = torch.equal(probe, first)
+        print(f"M={M}: probe rows {'bitwise equal' if same else 'DIFFER'} to M=16's", flush=True)
+        assert same
+        # the greedy path that never stores the logits agrees with the stored ones
+        rows = torch.arange(0, M, K + 1, device=device)
+        t = lm_head_sample(hidden, head, zeros, logits_indices=idx[rows])
+        assert torch.equal(t.cpu(), out[rows].float().cpu().argmax(-1))
+
+
+def test_lm_head_mixed_matches_separate_calls(device):
+    """lm_head_mixed (verify rows of D decode requests plus P finished prefill chunks in one GEMM) gives the
+    decisions of lm_head_verify on the decode rows and lm_head_sample on the prefill rows, greedy and sampled."""
+    D, k, P, V, H = 48, 4, 3, 3000, 512
+    N = D * (1 + k) + 700
+    hidden, weight, _ = _inputs(device, 31, D, k, V, H, N=N)
+    head = LMHeadVerifier(weight)
+    g = torch.Generator().manual_seed(32)
+    idx = torch.randperm(N, generator=g)[:D * (1 + k) + P].to(device)
+    drafts = torch.randint(0, V, (D, k), generator=g).to(device)
+    nd = torch.randint(0, k + 1, (D,), generator=g).to(device)
+    for temps_d, temps_p in [(torch.zeros(D), torch.zeros(P)),
+                             (torch.tensor([0.0, 1.0, 0.5] * 16), torch.tensor([0.0, 0.8, 1.0]))]:
+        u = torch.rand(D + P, k, generator=g).to(device)
+        e = torch.empty(D + P, V).exponential_(1, generator=g).to(device)
+        a, t, f = lm_head_mixed(hidden, head, idx, D, drafts, nd, temps_d.to(device), temps_p.to(device),
+                                uniforms=u, exp_noise=e)
+        a_ref, t_ref = lm_head_verify(hidden, head, drafts, nd, temps_d.to(device),
+                                      logits_indices=idx[:D * (1 + k)], uniforms=u[:D], exp_noise=e[:D])
+        f_ref = lm_head_sample(hidden, head, temps_p.to(device), logits_indices=idx[D * (1 + k):],
+                               exp_noise=e[D:])
+        assert a.cpu().tolist() == a_ref.cpu().tolist() and t.cpu().tolist() == t_ref.cpu().tolist()
+        assert f.cpu().tolist() == f_ref.cpu().tolist()
+    # k = 0 (nothing to verify: one row per decode request)
+    a, t, f = lm_head_mixed(hidden, head, idx[:D + P], D, None, None, torch.zeros(D, device=device),
+                            torch.zeros(P, device=device))
+    ref = lm_head_sample(hidden, head, torch.zeros(D + P, device=device), logits_indices=idx[:D + P])
+    assert a.cpu().tolist() == [0] * D and (t.cpu().tolist() + f.cpu().tolist()) == ref.cpu().tolist()
