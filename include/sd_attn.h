@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define SD_ABI_VERSION 1
+#define SD_ABI_VERSION 2
 
 #define SD_STATUS_OK 0
 #define SD_STATUS_BAD_ARGUMENT 1
@@ -205,9 +205,11 @@ int sd_verify_drafts(const void* logits, int32_t logits_dtype, int64_t logits_ro
  * GEMM's epilogue takes each row's first argmax. With temperatures, logits_out ([S*(K+1), vocab] bf16, row
  * stride >= vocab) is required and the sampled rows are decided by sd_verify_drafts's passes over it. The
  * other arguments and the outputs are sd_verify_drafts's. No counterpart in the reference for the packing (the
- * reference's F.linear reads the weight as stored). The workspace size depends on the CU count of the current
- * device (the GEMM's last round of workgroups may be split along hidden_dim, its fp32 sums kept there): size it
- * with that device current and call on a stream of the same device.
+ * reference's F.linear reads the weight as stored). A token row's logits depend on its hidden row, the weight and
+ * (vocab, hidden_dim) only, never on the call's row count (num_seqs * (K+1)) or the device's CU count: the
+ * vocabulary tiles of the GEMM's last round are split along hidden_dim by a rule of (vocab, hidden_dim) alone and
+ * their fp32 sums added in a fixed order in the workspace. K = 0 is plain sampling (Sampler.forward,
+ * sampler.py:7-16, on compute_logits' rows), so plain decode and verify steps read the same logits.
  */
 size_t sd_lm_head_packed_weight_size(int32_t vocab, int32_t hidden_dim);
 int sd_lm_head_pack_weight(const void* weight, int32_t vocab, int32_t hidden_dim, void* packed_weight, void* stream);
@@ -220,6 +222,32 @@ int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, int32_t hid
                       const float* exp_noise, int32_t num_seqs, int32_t num_draft_slots, void* logits_out,
                       int64_t logits_out_row_stride, int64_t* num_accepted, int64_t* next_token, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/*
+ * Linear layer with row-invariant results: out[m, n] = bf16(fp32 sum_k x[m, k] * w[n, k]), as F.linear in bf16
+ * computes the projections of nanovllm/layers/linear.py (the reference's qkv_proj, o_proj, gate_up_proj and
+ * down_proj, nanovllm/models/qwen3.py:47-63,115-126). It is the LM head's GEMM without the argmax: packed_weight
+ * is w [out_features, in_features] bf16 in sd_lm_head_pack_weight's layout (in_features a multiple of 32); x bf16
+ * with 16-byte aligned rows (row stride a multiple of 8 elements), out bf16 with any row stride >= out_features. Each output row depends on its
+ * input row and the weight only, never on `rows`: the library GEMM picks kernels (and summation orders) by the
+ * row count, which changes a model's greedy tokens with the batch; reference counterpart of the property:
+ * scripts/check_padding.py:46-52 (GEMMs, padded vs alone).
+ */
+size_t sd_linear_workspace_size(int32_t rows, int32_t out_features, int32_t in_features);
+int sd_linear(const void* x, int64_t x_row_stride, int32_t rows, const void* packed_weight, int32_t out_features,
+              int32_t in_features, void* out, int64_t out_row_stride, void* workspace, size_t workspace_bytes,
+              void* stream);
+
+/*
+ * RMSNorm over rows of `hidden` bf16 elements. Replaces RMSNorm.forward, nanovllm/layers/layernorm.py:16-38:
+ * residual == NULL: out = rms_forward(x); else s = x + residual (fp32), residual_out = bf16(s) and
+ * out = add_rms_forward's normalised s. weight bf16 [hidden]; hidden a multiple of 8, at most 16384; rows
+ * 16-byte aligned. out may be x and residual_out may be residual (in place). A row's result does not depend on
+ * `rows` (fixed summation order), unlike the library's reductions.
+ */
+int sd_rms_norm(const void* x, int64_t x_row_stride, const void* residual, int64_t residual_row_stride,
+                const void* weight, float eps, int32_t rows, int32_t hidden, void* out, int64_t out_row_stride,
+                void* residual_out, int64_t residual_out_row_stride, void* stream);
 
 /*
  * sd_verify_drafts without a workspace argument, for callers that cannot allocate device memory (code under

@@ -60,7 +60,7 @@ struct Args {
   uint16_t* logits;         // null, or [M, V] bf16 with row stride logits_stride
   int64_t logits_stride;
   int32_t logits_vec;       // rows 8-byte aligned: 4 entries per store
-  TileBest* best;           // [M][tiles]
+  TileBest* best;           // [M][tiles], or null (no argmax)
   int32_t tiles;            // vocabulary tiles of kN rows
   // Tiles full.. (the last, partial round of workgroups) are cut into `splits` ranges of H each, one
   // workgroup per range, so that the last round fills the GPU; such a workgroup writes its fp32 sums to
@@ -180,6 +180,7 @@ __device__ __forceinline__ TileBest block_best(const Args& a, const f32x16 (&acc
 // The four vocabulary waves' candidates of `rows` token rows (red[row][wave], in LDS, after a barrier), reduced
 // in wave order into best[m][tile] by threads 0.. of the workgroup.
 __device__ __forceinline__ void reduce_best(const Args& a, const TileBest* red, int rows, int m0, int tile) {
+  if (!a.best) return;  // a plain linear layer: the logits only
   for (int mr = threadIdx.x; mr < rows; mr += blockDim.x) {
     const int m = m0 + mr;
     if (m >= a.M) continue;

@@ -912,7 +912,7 @@ int64_t lm_head_mpad(int64_t M) {
 
 // The GEMM runs one workgroup per CU. When the last round of its tiles, on a GPU of kSplitCUs CUs (MI355X's
 // count), holds at most half as many tiles as there are CUs, those tiles are split along H into
-// min(4, kSplitCUs / tail, H / 32) ranges. The choice depends on (V, H) only, never on the call's token rows
+// min(8, kSplitCUs / tail, H / 64) ranges (3 for the Qwen3 LM heads: 82 tiles of 594 in the last round). The choice depends on (V, H) only, never on the call's token rows
 // or on the device it runs on, and every row of workgroups applies it: a token row's fp32 sums, and so its
 // logits, are the same in every call (greedy speculative and plain decoding rely on it).
 constexpr int kSplitCUs = 256;
@@ -924,7 +924,7 @@ LmSplit lm_head_split(int V, int H) {
   LmSplit r{tiles, 1};
   const int tail = tiles - (tiles - 1) / kSplitCUs * kSplitCUs;  // tiles of the last round, 1..kSplitCUs
   if (2 * tail > kSplitCUs) return r;
-  const int splits = std::min({4, kSplitCUs / tail, H / lmhead::kK});
+  const int splits = std::min({8, kSplitCUs / tail, H / (2 * lmhead::kK)});
   if (splits < 2) return r;
   r.full = tiles - tail;
   r.splits = splits;
@@ -950,6 +950,24 @@ LmLayout lm_layout(int S, int K, int V, int H) {
   L.hp = align256(L.info + (size_t)S * sizeof(SeqInfo));
   L.part = align256(L.hp + (size_t)lm_head_mpad(M) * H * 2);
   L.total = align256(L.part + part_bytes);
+  return L;
+}
+
+// Workspace of sd_linear: the packed rows, then the split tiles' fp32 sums.
+struct LinLayout {
+  size_t hp, part, total;
+};
+LinLayout lin_layout(int M, int N, int K) {
+  const int tiles = (N + lmhead::kN - 1) / lmhead::kN;
+  const LmSplit sp = lm_head_split(N, K);
+  const int MB = lm_head_mb(M);
+  const int64_t grid_rows = lm_head_mpad(M) / (64 * MB);
+  LinLayout L;
+  L.hp = 0;
+  L.part = align256((size_t)lm_head_mpad(M) * K * 2);
+  L.total = align256(L.part + (sp.splits > 1 ? (size_t)grid_rows * (tiles - sp.full) * sp.splits * lmhead::kWaves *
+                                                   2 * MB * 16 * kWave * sizeof(float)
+                                             : 0));
   return L;
 }
 
@@ -1178,4 +1196,51 @@ extern "C" int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, 
   if ((rc = check_launch("lm_head_merge"))) return rc;
   hipLaunchKernelGGL((verify_decide<SD_DTYPE_BF16, SD_DTYPE_BF16, false>), dim3(S), dim3(64), 0, s, p);
   return check_launch("verify_decide");
+}
+
+extern "C" size_t sd_linear_workspace_size(int32_t rows, int32_t out_features, int32_t in_features) {
+  if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % lmhead::kK) return 0;
+  return lin_layout(rows, out_features, in_features).total;
+}
+
+extern "C" int sd_linear(const void* x, int64_t x_row_stride, int32_t rows, const void* packed_weight,
+                         int32_t out_features, int32_t in_features, void* out, int64_t out_row_stride, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  const char* who = "sd_linear";
+  const int M = rows, N = out_features, K = in_features;
+  if (M < 0 || N <= 0 || K <= 0) return fail(kBadArgument, "%s: bad sizes (rows %d, out %d, in %d)", who, M, N, K);
+  if (K % lmhead::kK) return fail(kUnsupported, "%s: in_features %d is not a multiple of %d", who, K, lmhead::kK);
+  if (M == 0) return kOk;
+  if (M > 0x7fffffff / 64) return fail(kUnsupported, "%s: too many rows", who);
+  if (!x || !packed_weight || !out) return fail(kBadArgument, "%s: null pointer", who);
+  if (x_row_stride < K || out_row_stride < N)
+    return fail(kBadArgument, "%s: a row stride is smaller than the row", who);
+  if (((uintptr_t)x | (uintptr_t)packed_weight) % 16 || x_row_stride % 8 || (uintptr_t)out % 2)
+    return fail(kUnsupported, "%s: x needs 16-byte aligned rows (row stride a multiple of 8 elements)", who);
+  const LinLayout lay = lin_layout(M, N, K);
+  if (!workspace || workspace_bytes < lay.total)
+    return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
+  hipStream_t s = (hipStream_t)stream;
+  lmhead::Args a{};
+  a.Mpad = (int32_t)lm_head_mpad(M);
+  a.hp = (const uint16_t*)((uint8_t*)workspace + lay.hp);
+  a.M = M;
+  a.wp = (const uint16_t*)packed_weight;
+  a.V = N;
+  a.H = K;
+  a.logits = (uint16_t*)out;
+  a.logits_stride = out_row_stride;
+  a.logits_vec = (uintptr_t)out % 8 == 0 && out_row_stride % 4 == 0;
+  a.best = nullptr;
+  a.tiles = (N + lmhead::kN - 1) / lmhead::kN;
+  const LmSplit split = lm_head_split(N, K);
+  a.full = split.full;
+  a.splits = split.splits;
+  a.part = (float*)((uint8_t*)workspace + lay.part);
+  const int64_t hchunks = (int64_t)(K / 32) * a.Mpad * 4;
+  hipLaunchKernelGGL(lmhead::lm_head_pack_hidden, dim3((unsigned)((hchunks + 255) / 256)), dim3(256), 0, s,
+                     (const uint16_t*)x, x_row_stride, M, (const int64_t*)nullptr, a.M, a.Mpad, K, (uint16_t*)a.hp);
+  const int rc = check_launch("lm_head_pack_hidden");
+  if (rc) return rc;
+  return launch_lm_head(a, s);
 }

@@ -56,6 +56,10 @@ SIGNATURES = {
                                         _c_void_p]),
     "sd_draft_step_inputs": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _i32, _i32, _i32,
                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "sd_linear_workspace_size": (_size, [_i32, _i32, _i32]),
+    "sd_linear": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _i32, _i32, _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
+    "sd_rms_norm": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _f32, _i32, _i32, _c_void_p, _i64, _c_void_p,
+                           _i64, _c_void_p]),
     "sd_sample": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _c_void_p, _size,
                          _c_void_p]),
 }

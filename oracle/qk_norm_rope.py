@@ -7,6 +7,8 @@ Restates, on the CPU with the reference's eager PyTorch operations (fp32 math, t
                     freqs = t x inv_freq, cache = cat(cos, sin))
 * rms_norm          nanovllm/layers/layernorm.py:16-26 (RMSNorm.rms_forward: fp32 mean of squares,
                     x * rsqrt(var + eps), cast to the input dtype, then times the bf16 weight)
+* add_rms_norm      nanovllm/layers/layernorm.py:28-38 (RMSNorm.add_rms_forward: x + residual in fp32, the sum
+                    rounded as the new residual, the fp32 sum normalised as rms_norm does)
 * apply_rotary      nanovllm/layers/rotary_embedding.py:6-14 (neox halves: y1 = x1 cos - x2 sin,
                     y2 = x2 cos + x1 sin, fp32, cast back) and :37-48 (cos / sin rows picked by position)
 * qk_norm_rope_store nanovllm/models/qwen3.py:83-97 (pre_attn: split, q_norm / k_norm unless the model has
@@ -38,6 +40,16 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     var = xf.pow(2).mean(dim=-1, keepdim=True)
     xf = xf * torch.rsqrt(var + eps)
     return xf.to(orig) * weight
+
+
+def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """(normalised x + residual, x + residual rounded) with the reference's roundings (layernorm.py:28-38)."""
+    orig = x.dtype
+    xf = x.float() + residual.float()
+    res = xf.to(orig)
+    var = xf.pow(2).mean(dim=-1, keepdim=True)
+    xf = xf * torch.rsqrt(var + eps)
+    return xf.to(orig) * weight, res
 
 
 def apply_rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:

@@ -26,7 +26,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared_functions()
-    assert len(names) == 21, names
+    assert len(names) == 24, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -96,6 +96,19 @@ def test_bad_arguments_return_status(lib):
     assert rc == 1 and b"eps" in lib.sd_last_error()
     assert nr(None, 0, None, 0, None, 0, None, None, None, 1e-6, None, 100, None, 0, None, 0, None, None, 0, None,
               0, 32, 8, 128, None) == 0                                                    # nothing to do
+    rc = lib.sd_linear(None, 4096, 4, None, 6144, 100, None, 6144, None, 0, None)
+    assert rc == 2 and b"multiple of 32" in lib.sd_last_error()
+    rc = lib.sd_linear(None, 4096, 4, None, 6144, 4096, None, 6144, None, 0, None)
+    assert rc == 1 and b"null pointer" in lib.sd_last_error()
+    assert lib.sd_linear(None, 0, 0, None, 6144, 4096, None, 0, None, 0, None) == 0            # nothing to do
+    # packed rows [Mpad=64][4096] bf16, then [1 row of workgroups][16 split tiles][8 ranges] of fp32 sums
+    assert lib.sd_linear_workspace_size(1, 4096, 4096) == 64 * 4096 * 2 + 16 * 8 * 8 * 2 * 1 * 16 * 64 * 4
+    rn = lib.sd_rms_norm
+    rc = rn(None, 4096, None, 0, None, 1e-6, 4, 4100, None, 4096, None, 0, None)
+    assert rc == 2 and b"multiple of 8" in lib.sd_last_error()
+    rc = rn(None, 4096, ctypes.addressof(ws), 4096, None, 1e-6, 4, 4096, None, 4096, None, 0, None)
+    assert rc == 1 and b"together" in lib.sd_last_error()
+    assert rn(None, 0, None, 0, None, 1e-6, 0, 4096, None, 0, None, 0, None) == 0                 # nothing to do
     di = lib.sd_draft_step_inputs
     rc = di(None, None, None, 33, 256, None, 5, 1, 4, None, None, None, None, None)
     assert rc == 1 and b"bad sizes" in lib.sd_last_error()                   # more tokens than sequences

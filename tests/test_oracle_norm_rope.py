@@ -103,6 +103,30 @@ def test_rms_norm_scale_invariance_and_weight():
     assert torch.equal(onr.rms_norm(x, one * 2, 0.0), a * 2)      # the weight multiplies the rounded value
 
 
+def test_add_rms_norm_sum_rounding_and_zero_residual():
+    """add_rms_norm: the new residual is bf16(x + r) (the float64 sum rounded, where the fp32 sum is exact), the
+    output normalises the unrounded sum within the two roundings, a zero residual reduces it to rms_norm, and the
+    operands commute."""
+    g = torch.Generator().manual_seed(5)
+    H = 4096
+    x = torch.randn(16, H, generator=g).to(torch.bfloat16)
+    r = (torch.randn(16, H, generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.2 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    out, res = onr.add_rms_norm(x, r, w, 1e-6)
+    s = x.double() + r.double()
+    assert torch.equal(res, s.to(torch.bfloat16))
+    ref = s / torch.sqrt((s * s).mean(-1, keepdim=True) + 1e-6) * w.double()
+    err = (out.double() - ref).abs()
+    assert (err <= ref.abs() * (2 ** -7) + 1e-30).all()
+    # planted: normalising the rounded residual instead of the fp32 sum changes some rows
+    planted = onr.rms_norm(res, w, 1e-6)
+    assert not torch.equal(planted, out)
+    z_out, z_res = onr.add_rms_norm(x, torch.zeros_like(x), w, 1e-6)
+    assert torch.equal(z_res, x) and torch.equal(z_out, onr.rms_norm(x, w, 1e-6))
+    c_out, c_res = onr.add_rms_norm(r, x, w, 1e-6)
+    assert torch.equal(c_out, out) and torch.equal(c_res, res)
+
+
 # ------------------------------------------------------------------ rotary
 
 def _rope_inputs(seed, N=40, H=4, P=9000):
