@@ -14,12 +14,20 @@ Each layer's q/k RMSNorm, rotary embedding and KV store run in the runner's fuse
 on each token alone (no step metadata), so one recording serves every step padded to the same token count.
 The norms follow the reference's RMSNorm arithmetic (nanovllm/layers/layernorm.py:16-38: fp32 mean of squares,
 rsqrt, cast, times the weight); the GEMMs are torch's (hipBLASLt).
+
+row_invariant=True runs the projections through RowInvariantLinear (sd_linear) and the norms through
+sd_rms_norm instead: every op then computes a token's row the same way whatever the step's token count, so a
+token's hidden state, and the greedy token picked from it, do not depend on the batch. That is what makes
+greedy speculative decoding (1 + k rows per sequence) pick exactly the tokens of plain decoding (one row); with
+the library GEMMs and reductions, whose kernels change with the row count, near-ties can flip.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
 
+from nanovllm_amd.layers import layernorm
+from nanovllm_amd.layers.linear import RowInvariantLinear
 from nanovllm_amd.layers.rotary_embedding import RotaryEmbedding
 
 
@@ -49,7 +57,7 @@ class Qwen3Segments:
     def __init__(self, num_layers: int = 36, hidden: int = 4096, num_heads: int = 32, num_kv_heads: int = 8,
                  head_dim: int = 128, intermediate: int = 12288, vocab: int = 151936, eps: float = 1e-6,
                  rope_theta: float = 1e6, max_position: int = 40960, max_tokens: int = 2048, device=None,
-                 seed: int = 0):
+                 seed: int = 0, row_invariant: bool = False):
         dev = torch.device(device if device is not None else "cuda")
         self.L, self.hidden, self.Hq, self.Hkv, self.D = num_layers, hidden, num_heads, num_kv_heads, head_dim
         self.eps, self.device = eps, dev
@@ -70,6 +78,10 @@ class Qwen3Segments:
         self.final_norm = norm_w(hidden)
         self.lm_head = lin(vocab, hidden)
         self.cos_sin = RotaryEmbedding(head_dim, head_dim, max_position, rope_theta).cos_sin_cache.to(dev)
+        self.row_invariant = row_invariant
+        if row_invariant:   # the projections' weights packed once into the row-invariant GEMM's layout
+            for w in self.layers:
+                w.update({f"{name}_lin": RowInvariantLinear(w[name]) for name in ("qkv", "o", "gate_up", "down")})
         self.input_ids = torch.zeros(max_tokens, dtype=torch.int64, device=dev)
         self.residual = torch.zeros(max_tokens, hidden, dtype=torch.bfloat16, device=dev)
         self.hidden_out = torch.zeros(max_tokens, hidden, dtype=torch.bfloat16, device=dev)
@@ -78,22 +90,34 @@ class Qwen3Segments:
         """MixedStepRunner's pre_attn argument: (cos_sin_cache, per-layer (q_norm, k_norm), eps)."""
         return self.cos_sin, [(w["q_norm"], w["k_norm"]) for w in self.layers], self.eps
 
+    def _linear(self, x: torch.Tensor, w: dict, name: str, out: torch.Tensor | None = None) -> torch.Tensor:
+        if self.row_invariant:
+            return w[f"{name}_lin"](x, out=out)
+        if out is None:
+            return F.linear(x, w[name])
+        return torch.mm(x, w[name].t(), out=out)
+
+    def _norm(self, x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None = None):
+        if self.row_invariant:
+            return layernorm.rms_norm(x, weight, self.eps, residual)
+        return rms_norm(x, weight, self.eps) if residual is None else add_rms_norm(x, residual, weight, self.eps)
+
     def _post_attn(self, w: dict, o: torch.Tensor, residual: torch.Tensor):
         """Qwen3DecoderLayer.post_attn (qwen3.py:192-201)."""
-        h = F.linear(o, w["o"])
-        h, residual = add_rms_norm(h, residual, w["post_norm"], self.eps)
-        gate, up = F.linear(h, w["gate_up"]).chunk(2, -1)
-        return F.linear(F.silu(gate) * up, w["down"]), residual
+        h = self._linear(o, w, "o")
+        h, residual = self._norm(h, w["post_norm"], residual)
+        gate, up = self._linear(h, w, "gate_up").chunk(2, -1)
+        return self._linear(F.silu(gate) * up, w, "down"), residual
 
     def __call__(self, i: int, n: int, bufs: dict) -> None:
         if i == 0:
             h = F.embedding(self.input_ids[:n], self.embed)
-            x, residual = rms_norm(h, self.layers[0]["in_norm"], self.eps), h
+            x, residual = self._norm(h, self.layers[0]["in_norm"]), h
         else:
             h, residual = self._post_attn(self.layers[i - 1], bufs["o"][:n].view(n, -1), self.residual[:n])
             if i == self.L:
-                self.hidden_out[:n] = add_rms_norm(h, residual, self.final_norm, self.eps)[0]
+                self.hidden_out[:n] = self._norm(h, self.final_norm, residual)[0]
                 return
-            x, residual = add_rms_norm(h, residual, self.layers[i]["in_norm"], self.eps)
+            x, residual = self._norm(h, self.layers[i]["in_norm"], residual)
         self.residual[:n] = residual
-        torch.mm(x, self.layers[i]["qkv"].t(), out=bufs["qkv"][:n])
+        self._linear(x, self.layers[i], "qkv", out=bufs["qkv"][:n])
