@@ -19,6 +19,9 @@ Also reported (same JSON line):
   runtime (tok/s), its roofline fractions, the prefill kernel at GPU-filling sizes, and the whole step of a
   random-init Qwen3-8B-shaped model (36 layers run piecewise in the step's graph, then the LM head and the
   verifier);
+* whole-model verify (k = 4) and plain decode steps of the same model at B in {1, 16, 64} x context {256,
+  1024} (one HIP graph per step, then the LM head and the greedy decision), with the library GEMMs and with
+  the row-invariant projections and norms;
 * a CPU baseline: the oracle (PyTorch CPU restatement) timed on the headline workload for about 10 s on 16
   host threads.
 
@@ -471,13 +474,14 @@ def bench_prefill(dev):
     return res
 
 
-def bench_mixed_step_full(dev, layers=36, steps=5, warmup=2):
+def bench_mixed_step_full(dev, layers=36, steps=5, warmup=2, row_invariant=False):
     """The whole config-5 step: a random-init Qwen3-8B-shaped model (36 layers, hidden 4096, 32 q / 8 kv heads,
     MLP 12288, vocab 151936, bf16) run piecewise by the mixed-step runtime in one HIP graph per bucket
     (embedding, per layer: input norm + qkv GEMM, fused q/k norm + RoPE + KV store, varlen attention,
     o_proj + post norm + MLP; final norm), then, eagerly as the reference's run_mixed does, the LM head on the
     decode requests' verify rows and the greedy verifier (sd_lm_head_verify: one call, no logits written).
-    Reports the model step alone (graph replay) and the whole step, as query tokens per second."""
+    Reports the model step alone (graph replay) and the whole step, as query tokens per second. row_invariant:
+    the projections and norms through sd_linear / sd_rms_norm instead of the library's."""
     import torch
     from types import SimpleNamespace
     from nanovllm_amd import _lib
@@ -490,7 +494,7 @@ def bench_mixed_step_full(dev, layers=36, steps=5, warmup=2):
     W = math.ceil(max(lk) / BLOCK)
     kc, vc, tables = paged_cache(dev, lk, HKV, D, W=W, seed=5)
     caches = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(layers - 1)]
-    seg = Qwen3Segments(num_layers=layers, device=dev, seed=1)
+    seg = Qwen3Segments(num_layers=layers, device=dev, seed=1, row_invariant=row_invariant)
     runner = MixedStepRunner([SimpleNamespace(k_cache=a, v_cache=b) for a, b in caches], HQ, HKV, D, D ** -0.5,
                              block_size=BLOCK, max_num_batched_tokens=2048, max_num_seqs=64, table_width=W,
                              segment=seg, pre_attn=seg.pre_attn())
@@ -533,6 +537,75 @@ def bench_mixed_step_full(dev, layers=36, steps=5, warmup=2):
                timing="wall clock of back-to-back steps between synchronizations (the step's metadata copy, "
                       "one graph replay, then sd_lm_head_verify eagerly)")
     del caches, kc, vc, seg, runner, wp
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_decode_step_full(dev, layers=36, steps=5, warmup=2, k=4):
+    """Whole-model verify steps (1 + k rows per sequence: DecodeStepRunner graph replay, then sd_lm_head_verify)
+    against plain decode steps (one row: graph replay, then the LM head and the greedy sampler through the same
+    GEMM, K = 0) of a random-init Qwen3-8B-shaped model (36 layers), at B in {1, 16, 64} x context {256, 1024}:
+    the grid of the reference's step-cost runs (nanovllm/engine/model_runner.py:591-634 measure_step_costs; A100,
+    Qwen3-8B: B=64 ctx 1024 42.80 vs 18.17 ms). Each step: its metadata copy, the graph replay, the LM head
+    call; wall clock between synchronizations. Then the same grid with the row-invariant projections and norms
+    (greedy spec == plain bitwise), on a second copy of the model."""
+    import torch
+    from types import SimpleNamespace
+    from nanovllm_amd.engine.decode_step import DecodeStepRunner
+    from nanovllm_amd.engine.qwen3_segments import Qwen3Segments
+    from nanovllm_amd.layers.lm_head import LMHeadVerifier, lm_head_sample, lm_head_verify
+    Bmax, ctxs, batches = 64, (256, 1024), (1, 16, 64)
+    W = math.ceil((max(ctxs) + k + 1) / BLOCK)
+    NB = Bmax * W
+    caches = [SimpleNamespace(k_cache=torch.zeros(NB, BLOCK, HKV, D, dtype=torch.bfloat16, device=dev),
+                              v_cache=torch.zeros(NB, BLOCK, HKV, D, dtype=torch.bfloat16, device=dev))
+              for _ in range(layers)]
+    g = torch.Generator(device=dev).manual_seed(3)
+
+    def seqs_for(B, ctx):
+        return [SimpleNamespace(token_ids=[100 + i] * ctx, last_token=100 + i, num_tokens=ctx,
+                                block_table=list(range(i * W, (i + 1) * W)), draft_token_ids=[7] * k)
+                for i in range(B)]
+
+    def measure(model, head, B, ctx):
+        runner = measure.runners[id(model)]
+        seqs = seqs_for(B, ctx)
+        zeros = torch.zeros(B, device=dev)
+        drafts = torch.full((B, k), 7, dtype=torch.int64, device=dev)
+        nd = torch.full((B,), k, dtype=torch.int64, device=dev)
+        out = {}
+        for name, n in (("verify", 1 + k), ("plain", 1)):
+            layout = runner.prepare(seqs, n, with_drafts=n > 1)
+
+            def step():
+                h = runner.run(layout)
+                if n > 1:
+                    lm_head_verify(h, head, drafts, nd, zeros)
+                else:
+                    lm_head_sample(h, head, zeros)
+            wall, _ = timed(step, steps, warmup)
+            out[f"{name}_ms"] = round(wall * 1e3, 3)
+        out["verify_over_plain"] = round(out["verify_ms"] / out["plain_ms"], 3)
+        return out
+    measure.runners = {}
+
+    res = {}
+    for mode in ("library", "row_invariant"):
+        model = Qwen3Segments(num_layers=layers, device=dev, seed=1, max_tokens=Bmax * (1 + k),
+                              row_invariant=mode == "row_invariant")
+        head = LMHeadVerifier(model.lm_head)
+        measure.runners[id(model)] = DecodeStepRunner(caches, model, HQ, HKV, D, D ** -0.5, BLOCK, table_width=W,
+                                                      max_batch=Bmax, query_tokens=(1, 1 + k))
+        res[mode] = {f"B{B}_ctx{c}": measure(model, head, B, c) for c in ctxs for B in batches}
+        del measure.runners[id(model)], model, head
+        torch.cuda.empty_cache()
+    res["reference_a100_ms"] = {"B1_ctx1024": [12.05, 11.35], "B16_ctx1024": [16.81, 12.99],
+                                "B64_ctx1024": [42.80, 18.17], "B64_ctx256": [33.01, 13.88],
+                                "note": "[verify, plain] whole-step ms on A100 (CUDA graphs, Qwen3-8B weights), "
+                                        "other hardware: context only"}
+    res["timing"] = ("wall clock of back-to-back steps between synchronizations: metadata copy, one graph replay "
+                     "of the 36-layer model, the LM head with the greedy decision (k = 4 verify / plain)")
+    del caches
     torch.cuda.empty_cache()
     return res
 
@@ -700,7 +773,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="leave out the CPU baseline (for profiling)")
     ap.add_argument("--only", choices=["qk_norm_rope_store", "draft_step_inputs", "kv_store", "lm_head_verify",
                                        "verify_sampler", "mixed_step_full", "mixed_step_attention", "prefill_kernel",
-                                       "verify_attention_sweep"],
+                                       "verify_attention_sweep", "decode_step_full"],
                     help="run one secondary workload alone and print its JSON (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
@@ -723,10 +796,11 @@ def main():
               "kv_store": lambda: bench_store(dev, args.steps, args.warmup),
               "lm_head_verify": lambda: bench_lm_head_verify(dev),
               "verify_sampler": lambda: bench_sampler(dev, args.steps, args.warmup),
-              "mixed_step_full": lambda: bench_mixed_step_full(dev),
+              "mixed_step_full": lambda: [bench_mixed_step_full(dev), bench_mixed_step_full(dev, row_invariant=True)],
               "mixed_step_attention": lambda: bench_mixed_attention(dev, max(5, args.steps // 10), 2),
               "prefill_kernel": lambda: bench_prefill(dev),
-              "verify_attention_sweep": lambda: bench_verify_sweep(dev)}[args.only]
+              "verify_attention_sweep": lambda: bench_verify_sweep(dev),
+              "decode_step_full": lambda: bench_decode_step_full(dev)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
     head = bench_verify_attention(dev, args.steps, args.warmup)
@@ -779,6 +853,8 @@ def main():
             "note": "one layer's attention launch (planned work lists, caches cycled over 36 layers); combined_frac "
                     "= (prefill FLOPs / MFMA peak + decode bytes / HBM peak) / layer time"}
         result["mixed_step_full_model"] = bench_mixed_step_full(dev)
+        result["mixed_step_full_model_row_invariant"] = bench_mixed_step_full(dev, row_invariant=True)
+        result["decode_step_full_model"] = bench_decode_step_full(dev)
         result["prefill_kernel"] = bench_prefill(dev)
     if not args.skip_extras and not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(head["inputs"])
