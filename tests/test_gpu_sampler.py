@@ -180,8 +180,10 @@ def test_config4_full_vocab_vs_oracle(device, seed, T, dtype, with_draft, ragged
     print(f"seed {seed} T={T} {dtype} draft={with_draft} ragged={ragged} offset={offset} masked={masked}: "
           f"accepted {a.tolist()[:12]}... mismatches {bad}, within {ULPS} ulps of a flip {sorted(flagged)}",
           flush=True)
-    assert set(bad) <= flagged, (bad, flagged)
-    assert len(bad) <= 1
+    # exact: the kernel reproduces the reference's own outputs bit for bit (test_golden_full_vocab_exact), and
+    # on these ten batches it agrees with the oracle on every row; a mismatch prints whether the row lies within
+    # ULPS of a flip, to tell a rounding-order tie from a real error
+    assert not bad, (bad, flagged)
 
 
 def test_all_greedy_path_equals_general_path(device):
