@@ -869,7 +869,9 @@ __global__ __launch_bounds__(kStreamThreads, 1) void attn_stream(Params p) {
 // takes the lists interleaved, two prefill q-blocks then one residue item (each list in its own order,
 // longest first), then the rest of the longer list: the long prefill blocks start early without holding
 // every CU while the decode rows wait, so HBM keeps streaming under the prefill math (config-5 layer 59 ->
-// 49 us against the prefill list first). A residue item runs all eight residues in the workgroup (merged in
+// 49 us against the prefill list first). The q-blocks of sequences that see no key (the padding rows of a
+// graph bucket: they only write zeros) come after both lists, so that they do not shift the interleave
+// (they cost the 2048-token mixed layer 2 us, 45.5 against 43.5, in the interleave). A residue item runs all eight residues in the workgroup (merged in
 // LDS, two row tiles). Slots past both lists exit; the grid has kMixedSlack spare slots for a partial last
 // group.
 constexpr int kMixedPre = 2, kMixedRes = 1;
@@ -883,20 +885,29 @@ __global__ __launch_bounds__(kResidues * kWave, 2) void mixed_fwd(Params p, Pref
   // KV head fastest along the grid, rotated by one per batch of resident workgroups (see rotated_head).
   const int h = (int)((blockIdx.x % a.Hkv + blockIdx.x / p.wave_slots) % a.Hkv);
   const int x = blockIdx.x / a.Hkv;
-  const int np = *a.work_count, nr = *p.work_count;  // the plan's counts (each at most its grid share)
+  // The plan's counts (each at most its grid share): np prefill q-blocks, the first npk of them from sequences
+  // with keys (the rest see no key: a padded bucket's padding rows, which only write zeros), nr residue items.
+  const int np = a.work_count[0], npk = a.work_count[1], nr = *p.work_count;
   constexpr int G = kMixedPre + kMixedRes;
-  const int groups = min((np + kMixedPre - 1) / kMixedPre, (nr + kMixedRes - 1) / kMixedRes);
+  const int groups = min((npk + kMixedPre - 1) / kMixedPre, (nr + kMixedRes - 1) / kMixedRes);
   int pre = -1, res = -1;
   if (x < groups * G) {
     const int j = x / G, s = x % G;
-    if (s < kMixedPre)
-      pre = j * kMixedPre + s;
-    else
+    if (s < kMixedPre) {
+      if (j * kMixedPre + s < npk) pre = j * kMixedPre + s;
+    } else {
       res = j * kMixedRes + s - kMixedPre;
-  } else if (groups * kMixedPre < np) {
-    pre = groups * kMixedPre + x - groups * G;
+    }
   } else {
-    res = groups * kMixedRes + x - groups * G;
+    // then the rest of the longer list, and the zero-key q-blocks last, so that they shift nothing
+    const int y = x - groups * G;
+    const int rest_pre = max(npk - groups * kMixedPre, 0), rest_res = max(nr - groups * kMixedRes, 0);
+    if (y < rest_pre)
+      pre = groups * kMixedPre + y;
+    else if (y < rest_pre + rest_res)
+      res = groups * kMixedRes + y - rest_pre;
+    else
+      pre = npk + y - rest_pre - rest_res;
   }
   if (pre >= 0 && pre < np)
     prefill::prefill_body<kPaged, kPreRowGroups, kPreStageTiles>(a, lds, pre, h);
@@ -956,7 +967,8 @@ __global__ __launch_bounds__(256) void attn_combine(Params p) {
 // prefill kernel, its last q-block (the one that sees the most keys) first. With at most kPlanThreads
 // sequences, the sequences are taken in decreasing order of key count (ties by index; a bitonic sort in
 // LDS), so that the longest work items are dispatched first and the short ones fill the tail; with more,
-// in index order. One 1024-thread workgroup: each pass takes 1024 sequences (wave prefix sums, then the wave
+// in index order. The prefill count is written twice: all q-blocks, then those of sequences with keys (the
+// zero-key ones, sorted last, are dispatched after everything else). One 1024-thread workgroup: each pass takes 1024 sequences (wave prefix sums, then the wave
 // totals). The order changes only which workgroup computes an item, never an item's arithmetic.
 constexpr int kPlanThreads = 1024;
 __device__ __forceinline__ int wave_inclusive_sum(int x, int lane) {
@@ -1000,12 +1012,12 @@ __global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __res
                                                             int32_t* __restrict__ count_pre, int32_t max_pre) {
   constexpr int kPlanWaves = kPlanThreads / kWave;
   static_assert(kPlanThreads == 1024, "sort keys hold a 10-bit sequence index");
-  __shared__ int32_t wsum[2][kPlanWaves];
-  __shared__ int32_t carry[2];
+  __shared__ int32_t wsum[3][kPlanWaves];
+  __shared__ int32_t carry[3];
   __shared__ uint32_t keys[kPlanThreads];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const bool sorted = num_seqs <= kPlanThreads;
-  if (tid < 2) carry[tid] = 0;
+  if (tid < 3) carry[tid] = 0;
   if (sorted) {
     // key = (2^20 - 1 - key tiles) << 10 | sequence: ascending keys = descending work, then index order.
     uint32_t key = 0xFFFFFFFFu;
@@ -1022,18 +1034,23 @@ __global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __res
   for (int base = 0; base < num_seqs; base += kPlanThreads) {
     const int idx = base + tid;
     const int s = sorted ? (int)(keys[tid] & 1023u) : idx;
-    int Lq = 0;
-    if (idx < num_seqs) Lq = max(cu_q[s + 1] - cu_q[s], 0);
+    int Lq = 0, Lk = 0;
+    if (idx < num_seqs) {
+      Lq = max(cu_q[s + 1] - cu_q[s], 0);
+      Lk = cu_k[s + 1] - cu_k[s];
+    }
     const int nr = Lq > 0 && Lq <= kResidueMaxQ ? (Lq + P_res - 1) / P_res : 0;
     const int nq = Lq > kResidueMaxQ ? (Lq + P_pre - 1) / P_pre : 0;
     const int ir = wave_inclusive_sum(nr, lane);
     const int iq = wave_inclusive_sum(nq, lane);
+    const int ik = wave_inclusive_sum(Lk > 0 ? nq : 0, lane);
     if (lane == kWave - 1) {
       wsum[0][wave] = ir;
       wsum[1][wave] = iq;
+      wsum[2][wave] = ik;
     }
     __syncthreads();
-    int offr = carry[0], offq = carry[1], totr = 0, totq = 0;
+    int offr = carry[0], offq = carry[1], totr = 0, totq = 0, totk = 0;
     for (int w = 0; w < kPlanWaves; ++w) {
       if (w < wave) {
         offr += wsum[0][w];
@@ -1041,6 +1058,7 @@ __global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __res
       }
       totr += wsum[0][w];
       totq += wsum[1][w];
+      totk += wsum[2][w];
     }
     const int start_r = offr + ir - nr, start_q = offq + iq - nq;
     for (int i = 0; i < nr; ++i) {
@@ -1059,12 +1077,16 @@ __global__ __launch_bounds__(kPlanThreads) void varlen_plan(const int32_t* __res
     if (tid == 0) {
       carry[0] += totr;
       carry[1] += totq;
+      carry[2] += totk;
     }
     __syncthreads();
   }
   if (tid == 0) {
     *count_res = min(carry[0], max_res);
-    *count_pre = min(carry[1], max_pre);
+    count_pre[0] = min(carry[1], max_pre);
+    // q-blocks of sequences with keys: a prefix of the list when it is sorted by key count (zero-key ones
+    // last); in index order they may sit anywhere, and all count as keyed
+    count_pre[1] = sorted ? min(carry[2], max_pre) : count_pre[0];
   }
 }
 
@@ -1141,7 +1163,7 @@ Layout workspace_layout(int64_t items, int Hkv, int rows_alloc, bool partials, b
   L.count = align256(L.work + (varlen ? (size_t)items * 2 * sizeof(int32_t) : 0));
   L.work_pre = align256(L.count + (varlen ? sizeof(int32_t) : 0));
   L.count_pre = align256(L.work_pre + (varlen ? (size_t)pre_items * 2 * sizeof(int32_t) : 0));
-  L.order = align256(L.count_pre + (varlen ? sizeof(int32_t) : 0));
+  L.order = align256(L.count_pre + (varlen ? 2 * sizeof(int32_t) : 0));  // all q-blocks, those with keys
   L.total = align256(L.order + (size_t)(order_len ? order_len + 1 : 0) * sizeof(int32_t));  // + load-policy flag
   return L;
 }
