@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 #include "prefill_attention.h"
 #include "sd_common.h"
@@ -54,26 +55,33 @@ constexpr int kMlBytes = kResidues * kMaxRows * 2 * 4;
 constexpr int kMergeRows = 32;                 // rows merged in LDS per pass (two row tiles)
 constexpr int kObBytes = kResidues * kMergeRows * kObRow * 4;
 
-// LDS of a workgroup with `waves` waves: one V buffer per wave (when the workgroup merges all eight
-// residues the same bytes then hold every residue's O), the merge's (max, sum) table, and the item's
-// block ids.
-constexpr int stage_bytes(int waves) {
-  return waves == kResidues ? (waves * kVBuf > kObBytes ? waves * kVBuf : kObBytes) : waves * kVBuf;
+// LDS of a workgroup with `waves` waves: the V buffers, one per wave, or two with the two-tiles-ahead
+// pipeline (`deep`; when the workgroup merges all eight residues the same bytes then hold every residue's
+// O), the merge's (max, sum) table, and the item's block ids.
+constexpr int stage_bytes(int waves, bool deep = false) {
+  return waves == kResidues ? ((deep ? 2 : 1) * waves * kVBuf > kObBytes ? (deep ? 2 : 1) * waves * kVBuf : kObBytes)
+                            : (deep ? 2 : 1) * waves * kVBuf;
 }
 constexpr int ml_bytes(int waves) { return waves == kResidues ? kMlBytes : 0; }
-constexpr int lds_bytes(int waves) { return stage_bytes(waves) + ml_bytes(waves) + kMaxBlocks * 4; }
-// Three and four row tiles read Q from LDS at every tile instead of holding it in registers (16 registers per
-// row tile), so that three fit in 256 registers and run two waves per SIMD. Q rows of 256 B, the 16-byte
-// chunk c of row r at c ^ (r % 16): the 16 lanes of a read take 16 different chunks. With eight waves the Q
-// rows sit in the stage bytes past the V buffers, which only the merge uses; otherwise past the block ids.
-constexpr int q_lds_bytes(int rt) { return rt >= 3 ? rt * 16 * kD * 2 : 0; }
-constexpr int q_lds_offset(int waves) { return waves == kResidues ? waves * kVBuf : lds_bytes(waves); }
-constexpr int lds_bytes_rt(int waves, int rt) {
-  return waves == kResidues ? lds_bytes(waves) : lds_bytes(waves) + q_lds_bytes(rt);
+constexpr int lds_bytes(int waves, bool deep = false) {
+  return stage_bytes(waves, deep) + ml_bytes(waves) + kMaxBlocks * 4;
 }
-static_assert(kResidues * kVBuf + q_lds_bytes(4) <= stage_bytes(kResidues), "Q rows fit past the V buffers");
+// Three and four row tiles read Q from LDS at every tile instead of holding it in registers (16 registers per
+// row tile), so that three fit in 256 registers and run two waves per SIMD. Q rows of 256 B past the block
+// ids, the 16-byte chunk c of row r at c ^ (r % 16): the 16 lanes of a read take 16 different chunks.
+// The two-tiles-ahead pipeline holds two tiles' K in registers and reads Q from LDS too, whatever RT.
+constexpr bool q_in_lds(int rt, bool deep = false) { return deep || rt >= 3; }
+constexpr int q_lds_bytes(int rt, bool deep = false) { return q_in_lds(rt, deep) ? rt * 16 * kD * 2 : 0; }
+constexpr int q_lds_offset(int waves, bool deep = false) { return lds_bytes(waves, deep); }
+constexpr int lds_bytes_rt(int waves, int rt, bool deep = false) {
+  return lds_bytes(waves, deep) + q_lds_bytes(rt, deep);
+}
+static_assert(lds_bytes_rt(kResidues, 3, true) <= 160 * 1024, "eight waves with three row tiles fit the LDS");
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+// Cache-policy operand of global_load_lds: the non-temporal bit (the policy kv_load's non-temporal loads get).
+constexpr int kCpolNT = 2;
 
 struct Params {
   const uint16_t* q;
@@ -189,13 +197,14 @@ __device__ __forceinline__ float merge_scale(float m_r, float M) {
 }
 
 // One (item, KV head h) with the workgroup's kWaves waves, owning residues bx*kWaves .. +kWaves-1; `lds`
-// holds lds_bytes_rt(kWaves, RT). (kCaller only separates the instantiations made from different kernels: the
+// holds lds_bytes_rt(kWaves, RT, kDeep). kDeep: tiles stream two ahead of the math instead of one (V through
+// global_load_lds), the same arithmetic in the same order. (kCaller only separates the instantiations made from different kernels: the
 // host compilation pass rejects one instantiation reached from two kernels.)
-template <int RT, bool kVarlen, bool kPaged, int kWaves, int kCaller = 0, bool kNT = false>
+template <int RT, bool kVarlen, bool kPaged, int kWaves, int kCaller = 0, bool kNT = false, bool kDeep = false>
 __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int item, int h, int bx) {
   constexpr bool kMergeHere = kWaves == kResidues;
-  constexpr int kStageBytes = stage_bytes(kWaves);
-  constexpr bool kQLds = q_lds_bytes(RT) > 0;
+  constexpr int kStageBytes = stage_bytes(kWaves, kDeep);
+  constexpr bool kQLds = q_in_lds(RT, kDeep);
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -211,10 +220,12 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   constexpr int kBlkPerThread = (kMaxBlocks + kWaves * kWave - 1) / (kWaves * kWave);
   int32_t blk_pre[kBlkPerThread];
   const int nblk_row = min(p.table_width, kMaxBlocks);
-  // This wave's first tile (tile `residue`) lies in table entry first_bi; its id is read with the row, as
-  // a scalar load, so that the tile's K and V loads can go out before the row reaches LDS.
+  // This wave's first two tiles (tiles `residue` and residue + 8) lie in table entries first_bi and
+  // second_bi; their ids are read with the row, as scalar loads, so that the tiles' K and V loads can go out
+  // before the row reaches LDS.
   const int first_bi = kPaged ? residue * kTile / p.block_size : 0;
-  int32_t first_blk = -1;
+  const int second_bi = kPaged ? (residue + kResidues) * kTile / p.block_size : 0;
+  int32_t first_blk = -1, second_blk = -1;
   if (kPaged) {
     int seq = 0;
     bool listed = true;
@@ -233,7 +244,10 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
       const int32_t id = p.block_tables[(int64_t)seq * p.table_width + min(b, nblk_row - 1)];
       blk_pre[i] = listed && b < nblk_row ? id : -1;
     }
-    if (listed) first_blk = p.block_tables[(int64_t)seq * p.table_width + min(first_bi, nblk_row - 1)];
+    if (listed) {
+      first_blk = p.block_tables[(int64_t)seq * p.table_width + min(first_bi, nblk_row - 1)];
+      second_blk = p.block_tables[(int64_t)seq * p.table_width + min(second_bi, nblk_row - 1)];
+    }
   }
   const Item it = describe<kVarlen>(p, item);
   if (!it.valid) {
@@ -242,7 +256,7 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
     if constexpr (kPaged) {
 #pragma unroll
       for (int i = 0; i < kBlkPerThread; ++i) asm volatile("" : : "v"(blk_pre[i]));
-      asm volatile("" : : "s"(first_blk));
+      asm volatile("" : : "s"(first_blk), "s"(second_blk));
     }
     return;
   }
@@ -254,7 +268,7 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   // (B of S^T): lane holds row 16*rt + r16, d = 32*ks + 8*grp + e.
   int lim[RT];
   bf16x8 qv[kQLds ? 1 : RT][4];
-  uint8_t* qlds = lds + q_lds_offset(kWaves);
+  uint8_t* qlds = lds + q_lds_offset(kWaves, kDeep);
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int row = rt * 16 + r16;
@@ -309,7 +323,7 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
     for (int dt = 0; dt < 8; ++dt) o[dt][rt] = f32x4{};
   }
 
-  uint8_t* vbuf = lds + wave * kVBuf;
+  uint8_t* const vring = lds + wave * (kDeep ? 2 : 1) * kVBuf;  // this wave's V buffer(s)
   // V^T reads (ds_read_b64_tr_b16): source lane reads 4 d of key tl (+16 for the second half) at
   // d = 16*dt + 4*(lane%4): chunk 2*dt + (lane%4)/2, byte 8*(lane%2) inside it.
   // That chunk, (2 dt + (lane%4)/2) ^ 2 (tl%8), is 2 (dt ^ (tl%8)) + (lane%4)/2: one xor per read from two
@@ -347,7 +361,17 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   };
   auto tile_blk = [&](int jt) {
     const int bi = jt * kTile / p.block_size;
-    return kPaged ? (bi < nblk_row ? blk_ids[bi] : -1) : 0;
+    if constexpr (kPaged && kDeep) {
+      // inline asm read (a compiler-visible LDS read would wait for the V loads writing LDS in flight); the
+      // ids were stored before the workgroup's barrier
+      if (bi >= nblk_row) return -1;
+      int32_t id;
+      const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const int32_t*)(blk_ids + bi);
+      asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(id) : "v"(a) : "memory");
+      return id;
+    } else {
+      return kPaged ? (bi < nblk_row ? blk_ids[bi] : -1) : 0;
+    }
   };
   // K of a tile into registers (A of S^T): key 16*kt + r16, d = 32*ks + 8*grp + e; 32-bit lane offsets.
   const uint32_t k_off0 = (uint32_t)(r16 * ksb) + 16 * grp;
@@ -355,19 +379,45 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
   auto load_k = [&](const TileSrc& ts, bf16x8 (&kr)[2][4]) {
     const uint32_t off0 = r16 < ts.nvalid ? k_off0 : 16 * grp;
     const uint32_t off1 = 16 + r16 < ts.nvalid ? k_off1 : 16 * grp;
+    if constexpr (kDeep) {
+      // inline asm loads: next to the V loads into LDS in flight, the compiler would wait for every load
+      // before any use of the K registers; the step's own vmcnt wait covers them
+      const uint64_t base = (uint64_t)(uintptr_t)ts.kb;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      kr[0][ks] = kv_load<kNT, bf16x8>(ts.kb + off0 + 64 * ks);
-      kr[1][ks] = kv_load<kNT, bf16x8>(ts.kb + off1 + 64 * ks);
+      for (int ks = 0; ks < 4; ++ks) {
+        asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(kr[0][ks]) : "v"(off0), "s"(base), "i"(64 * ks)
+                     : "memory");
+        asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(kr[1][ks]) : "v"(off1), "s"(base), "i"(64 * ks)
+                     : "memory");
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        kr[0][ks] = kv_load<kNT, bf16x8>(ts.kb + off0 + 64 * ks);
+        kr[1][ks] = kv_load<kNT, bf16x8>(ts.kb + off1 + 64 * ks);
+      }
     }
   };
-  // V of a tile: 16-byte register loads (lane loads key t = 4*qd + lane/16, chunk (lane%16) ^ 2*(t%8),
-  // so that the later LDS store of its register to slot lane%16 lands XOR-swizzled); t%8 only depends on
-  // the parity of qd. Stored to this wave's LDS buffer once the previous tile's V^T has been read.
+  // V of a tile straight into one of this wave's LDS buffers (global_load_lds: lane L's 16 bytes land at
+  // the instruction's base + 16 L): lane loads key t = 4*qd + lane/16, chunk (lane%16) ^ 2*(t%8), so that
+  // slot lane%16 of row-group qd holds it XOR-swizzled; t%8 only depends on the parity of qd. No registers
+  // hold V on its way, which leaves room for a second tile's K: two tiles in flight per wave.
   const int vf_key = lane / 16;
   const int vf_slot = lane % 16;
   const uint32_t v_c0 = 16 * (vf_slot ^ (2 * vf_key)), v_c1 = 16 * (vf_slot ^ (2 * (4 + vf_key)));
   const uint32_t v_off0 = (uint32_t)(vf_key * vsb) + v_c0, v_off1 = (uint32_t)(vf_key * vsb) + v_c1;
+  auto dma_v = [&](const TileSrc& ts, uint8_t* vb) {
+#pragma unroll
+    for (int qd = 0; qd < 8; ++qd) {
+      const bool valid = 4 * qd + vf_key < ts.nvalid;
+      // a wave-uniform base plus a 32-bit lane offset (the scalar-base addressing form)
+      const uint32_t off = valid ? (uint32_t)(4 * qd * vsb) + ((qd % 2) ? v_off1 : v_off0) : ((qd % 2) ? v_c1 : v_c0);
+      __builtin_amdgcn_global_load_lds((const void*)(ts.vb + off), (lds_void*)(vb + 1024 * qd), 16, 0,
+                                       kNT ? kCpolNT : 0);
+    }
+  };
+  // The classic path: V as 16-byte register loads to the same lanes and slots, stored to the wave's first
+  // buffer once the previous tile's V^T has been read.
   auto load_v = [&](const TileSrc& ts, u32x4 (&vs)[8]) {
 #pragma unroll
     for (int qd = 0; qd < 8; ++qd) {
@@ -376,12 +426,17 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
       vs[qd] = kv_load<kNT, u32x4>(ts.vb + (valid ? (int64_t)(4 * qd) * vsb : 0) + off);
     }
   };
-  auto store_v = [&](const u32x4 (&vs)[8], bool ok) {
+  auto store_v = [&](const u32x4 (&vs)[8], bool ok, uint8_t* vb) {
 #pragma unroll
-    for (int qd = 0; qd < 8; ++qd) *(u32x4*)(vbuf + 1024 * qd + 16 * lane) = ok ? vs[qd] : u32x4{0, 0, 0, 0};
+    for (int qd = 0; qd < 8; ++qd) *(u32x4*)(vb + 1024 * qd + 16 * lane) = ok ? vs[qd] : u32x4{0, 0, 0, 0};
   };
-  // V^T operand of d-tile dt (16 d x 32 keys) from this wave's LDS buffer: two transposed reads.
-  auto read_vt = [&](int dt) {
+  // A tile whose block id is invalid: its V (read from block 0) is replaced by zeros.
+  auto zero_v = [&](uint8_t* vb) {
+#pragma unroll
+    for (int qd = 0; qd < 8; ++qd) *(u32x4*)(vb + 1024 * qd + 16 * lane) = u32x4{0, 0, 0, 0};
+  };
+  // V^T operand of d-tile dt (16 d x 32 keys) from V buffer vbuf: two transposed reads.
+  auto read_vt = [&](const uint8_t* vbuf, int dt) {
     const uint32_t off = vt_off(dt);
     const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(vbuf + off));
     const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -390,20 +445,57 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
     return __builtin_bit_cast(bf16x8, e8);
   };
 
+  // V^T reads of the deep path: inline asm (the compiler would otherwise wait for every V load in flight
+  // before reading any buffer), four d-tiles at a time, their results passed through one lgkmcnt(0).
+  auto vt_frags4 = [&](const uint8_t* vbuf, int dt0, bf16x8 (&vt)[4]) {
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)vbuf;
+    u32x2 lo[4], hi[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      lo[d] = ds_read_tr16<0>(base + vt_off(dt0 + d));
+      hi[d] = ds_read_tr16<16 * 256>(base + vt_off(dt0 + d));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(lo[0]), "+v"(lo[1]), "+v"(lo[2]), "+v"(lo[3]), "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]),
+                   "+v"(hi[3])
+                 :
+                 : "memory");
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const u32x4 w = {lo[d][0], lo[d][1], hi[d][0], hi[d][1]};
+      vt[d] = __builtin_bit_cast(bf16x8, w);
+    }
+  };
   // One tile: S^T from the K registers, then (registers free) the next tile's K loads, then the online
   // softmax and O^T += V^T P^T.
-  auto compute = [&](int jt, bool tile_ok, bf16x8 (&kr)[2][4], bool has_next, const TileSrc& next) {
+  auto compute = [&](int jt, bool tile_ok, bf16x8 (&kr)[2][4], const uint8_t* vbuf, bool has_next,
+                     const TileSrc& next) {
     const int t0 = jt * kTile;
     // S^T of row tile rt into s[.][rt] (or s[.][0] when the row tiles are interleaved).
     constexpr bool kInterleave = kQLds;  // three or four row tiles: S^T of one row tile live at a time
     f32x4 s[2][kInterleave ? 1 : RT];
     auto scores = [&](int rt, int slot) {
       s[0][slot] = s[1][slot] = f32x4{};
+      if constexpr (kDeep) {
+        // inline asm reads (a compiler-visible LDS read would wait for the V loads writing LDS in flight)
+        bf16x8 qf[4];
+        const uint32_t qa = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)qlds +
+                            (rt * 16 + r16) * 256;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 qf = q_frag(rt, ks);
-        s[0][slot] = mfma16(kr[0][ks], qf, s[0][slot]);
-        s[1][slot] = mfma16(kr[1][ks], qf, s[1][slot]);
+        for (int ks = 0; ks < 4; ++ks) qf[ks] = ds_read_b128(qa + 16 * ((4 * ks + grp) ^ r16));
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]) : : "memory");
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          s[0][slot] = mfma16(kr[0][ks], qf[ks], s[0][slot]);
+          s[1][slot] = mfma16(kr[1][ks], qf[ks], s[1][slot]);
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 qf = q_frag(rt, ks);
+          s[0][slot] = mfma16(kr[0][ks], qf, s[0][slot]);
+          s[1][slot] = mfma16(kr[1][ks], qf, s[1][slot]);
+        }
       }
     };
     if constexpr (!kInterleave) {
@@ -452,58 +544,152 @@ __device__ __forceinline__ void attn_body(const Params& p, uint8_t* lds, int ite
       w[3] = cvt_bf16x2(x[6], x[7]);
       pb[rt] = __builtin_bit_cast(bf16x8, w);
     }
+    if constexpr (kDeep) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const bf16x8 vt = read_vt(dt);
+      for (int dt0 = 0; dt0 < 8; dt0 += 4) {
+        bf16x8 vt[4];
+        vt_frags4(vbuf, dt0, vt);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(vt, pb[rt], o[dt][rt]);
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) o[dt0 + d][rt] = mfma16(vt[d], pb[rt], o[dt0 + d][rt]);
+      }
+    } else {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const bf16x8 vt = read_vt(vbuf, dt);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) o[dt][rt] = mfma16(vt, pb[rt], o[dt][rt]);
+      }
     }
   };
 
-  // The loop body issues its loads unconditionally and the last tile is peeled: with a conditional load
-  // in the body the compiler's wait counts must cover the path without it and would wait for the next
-  // tile's V before this tile's S^T.
-  bf16x8 kreg[2][4];
-  u32x4 vstage[8];
-  int j = residue;
-  bool cur_ok = true;
-  {
-    // The first tile from first_blk. Paged, a wave without tiles loads tile 0 of block 0 and never uses
-    // it: loads on every path keep the waits before the LDS stores below exact.
-    const bool has_tile = j < end_tile;
-    const int blk0 = kPaged && has_tile && first_bi < nblk_row ? first_blk : -1;
-    const TileSrc ts = tile_src(has_tile ? j : 0, __builtin_amdgcn_readfirstlane(blk0));
-    if (kPaged || has_tile) {
-      load_v(ts, vstage);
-      load_k(ts, kreg);
+  const int nt = residue < end_tile ? (end_tile - 1 - residue) / kResidues + 1 : 0;  // this wave's tiles
+  if constexpr (!kDeep) {
+    // One tile ahead: while tile j is computed, tile j+8's V is in flight (registers) and its K goes out as
+    // soon as S^T has freed the K registers. The loop body issues its loads unconditionally and the last
+    // tile is peeled: with a conditional load in the body the compiler's wait counts must cover the path
+    // without it and would wait for the next tile's V before this tile's S^T.
+    bf16x8 kreg[2][4];
+    u32x4 vstage[8];
+    int j = residue;
+    bool cur_ok = true;
+    {
+      // The first tile from first_blk. Paged, a wave without tiles loads tile 0 of block 0 and never uses
+      // it: loads on every path keep the waits before the LDS stores below exact.
+      const bool has_tile = j < end_tile;
+      const int blk0 = kPaged && has_tile && first_bi < nblk_row ? first_blk : -1;
+      const TileSrc ts = tile_src(has_tile ? j : 0, __builtin_amdgcn_readfirstlane(blk0));
+      if (kPaged || has_tile) {
+        load_v(ts, vstage);
+        load_k(ts, kreg);
+      }
+      cur_ok = ts.ok;
     }
-    cur_ok = ts.ok;
-  }
-  // The item's block ids in LDS for the later tiles (all kMaxBlocks entries, -1 past the row).
-  if (kPaged) {
-    static_assert(kBlkPerThread * kWaves * kWave == kMaxBlocks, "one id per thread and step");
+    // The item's block ids in LDS for the later tiles (all kMaxBlocks entries, -1 past the row).
+    if (kPaged) {
+      static_assert(kBlkPerThread * kWaves * kWave == kMaxBlocks, "one id per thread and step");
 #pragma unroll
-    for (int i = 0; i < kBlkPerThread; ++i) blk_ids[tid + i * kWaves * kWave] = blk_pre[i];
-    __syncthreads();
+      for (int i = 0; i < kBlkPerThread; ++i) blk_ids[tid + i * kWaves * kWave] = blk_pre[i];
+      __syncthreads();
+    }
+    while (j + kResidues < end_tile) {
+      const int blk_next = tile_blk(j + kResidues);
+      lds_wave_fence();                  // previous tile's V^T reads (and the block id read) are complete
+      store_v(vstage, cur_ok, vring);    // waits for this tile's V registers
+      const TileSrc next = tile_src(j + kResidues, __builtin_amdgcn_readfirstlane(blk_next));
+      load_v(next, vstage);              // next tile's V in flight during this tile's math
+      __builtin_amdgcn_sched_barrier(0);  // keep those loads ahead of the S^T MFMAs
+      lds_wave_fence();                  // the tile is in LDS before any lane reads it
+      compute(j, cur_ok, kreg, vring, true, next);
+      cur_ok = next.ok;
+      j += kResidues;
+    }
+    if (j < end_tile) {
+      lds_wave_fence();
+      store_v(vstage, cur_ok, vring);
+      lds_wave_fence();
+      compute(j, cur_ok, kreg, vring, false, TileSrc{});
+    }
+  } else {
+    // Two tiles ahead: while tile i is computed, tile i+1's K (registers) and V (LDS, global_load_lds) are in
+    // flight, and tile i+2's loads go out as soon as tile i frees their registers (K, after S^T) and buffer
+    // (V, after its V^T reads). K of even and odd tiles alternates between two register sets and V between
+    // the two buffers, so the second set costs the registers that staged V in the classic path. No load
+    // goes past the wave's last tile (the wave would wait for its round trip before the merge).
+    uint8_t* const vb0 = vring;
+    uint8_t* const vb1 = vring + kVBuf;
+    bf16x8 ka[2][4], kb[2][4];
+    bool ok0 = true, ok1 = true;
+    // Past the wave's last tile a step still issues its sixteen loads (static counts: the compiler's waits for K
+    // stay exact with two copies of the step), from one L2-hot 1 KB piece: the first row of block 0 of this
+    // head, the same for every such load; never used.
+    TileSrc dummy{};
+    dummy.kb = (const uint8_t*)p.k + h * kD * 2;
+    dummy.vb = (const uint8_t*)p.v + h * kD * 2;
+    dummy.nvalid = 0;
+    dummy.ok = true;
+    TileSrc t0 = dummy, t1 = dummy;
+    {
+      const int blk0 = kPaged && nt > 0 && first_bi < nblk_row ? first_blk : -1;
+      const int blk1 = kPaged && nt > 1 && second_bi < nblk_row ? second_blk : -1;
+      if (nt > 0) t0 = tile_src(residue, __builtin_amdgcn_readfirstlane(blk0));
+      if (nt > 1) t1 = tile_src(residue + kResidues, __builtin_amdgcn_readfirstlane(blk1));
+      if (kPaged || nt > 0) {  // K into registers now; V (into LDS) after the block ids' barrier below
+        load_k(t0, ka);
+        load_k(t1, kb);
+      }
+      ok0 = t0.ok;
+      ok1 = t1.ok;
+    }
+    if (kPaged) {
+      static_assert(kBlkPerThread * kWaves * kWave == kMaxBlocks, "one id per thread and step");
+#pragma unroll
+      for (int i = 0; i < kBlkPerThread; ++i) blk_ids[tid + i * kWaves * kWave] = blk_pre[i];
+      __syncthreads();
+    }
+    if (kPaged || nt > 0) {
+      dma_v(t0, vb0);
+      dma_v(t1, vb1);
+    }
+    // Step i: wait for tile i, compute it when it is one of the wave's tiles, and send tile i+2's loads (or the
+    // stand-ins) into the registers and buffer it frees.
+    // Straight-line (no branch around the math, so the compiler's waits for K stay exact): a step past the
+    // wave's last tile computes a tile whose keys are all masked and whose V is zero, which leaves the row's
+    // max, sum and O bitwise as they are.
+    auto step = [&](int i, bf16x8 (&kr)[2][4], uint8_t* vb, bool& ok) {
+      const int jt = residue + kResidues * i;
+      TileSrc next = dummy;
+      if (i + 2 < nt) next = tile_src(jt + 2 * kResidues, __builtin_amdgcn_readfirstlane(tile_blk(jt + 2 * kResidues)));
+      const bool tile_ok = i < nt && ok;
+      // Loads issued after tile i's V: tile i+1's K and V (16), except for tile 0, whose V goes out after the
+      // barrier, behind tile 1's K: only tile 1's V (8) follows it.
+      if (i == 0)
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      if (!tile_ok) zero_v(vb);
+      lds_wave_fence();
+      compute(jt, tile_ok, kr, vb, true, next);
+      lds_wave_fence();  // tile i's V^T reads are done: its buffer takes tile i+2
+      dma_v(next, vb);
+      ok = next.ok;
+    };
+    for (int i = 0; i < nt; i += 2) {
+      step(i, ka, vb0, ok0);
+      step(i + 1, kb, vb1, ok1);
+    }
+    // The last steps' K loads (never used) are still in flight: both register sets stay allocated until they
+    // have landed, so that no other value takes those registers meanwhile.
+    asm volatile("s_waitcnt vmcnt(0)"
+                 :
+                 : "v"(ka[0][0]), "v"(ka[0][1]), "v"(ka[0][2]), "v"(ka[0][3]), "v"(ka[1][0]), "v"(ka[1][1]),
+                   "v"(ka[1][2]), "v"(ka[1][3]), "v"(kb[0][0]), "v"(kb[0][1]), "v"(kb[0][2]), "v"(kb[0][3]),
+                   "v"(kb[1][0]), "v"(kb[1][1]), "v"(kb[1][2]), "v"(kb[1][3])
+                 : "memory");
   }
-  while (j + kResidues < end_tile) {
-    const int blk_next = tile_blk(j + kResidues);
-    lds_wave_fence();          // previous tile's V^T reads (and the block id read) are complete
-    store_v(vstage, cur_ok);   // waits for this tile's V registers
-    const TileSrc next = tile_src(j + kResidues, __builtin_amdgcn_readfirstlane(blk_next));
-    load_v(next, vstage);      // next tile's V in flight during this tile's math
-    __builtin_amdgcn_sched_barrier(0);  // keep those loads ahead of the S^T MFMAs
-    lds_wave_fence();          // the tile is in LDS before any lane reads it
-    compute(j, cur_ok, kreg, true, next);
-    cur_ok = next.ok;
-    j += kResidues;
-  }
-  if (j < end_tile) {
-    lds_wave_fence();
-    store_v(vstage, cur_ok);
-    lds_wave_fence();
-    compute(j, cur_ok, kreg, false, TileSrc{});
-  }
+  // every load has landed (also the unused ones): the V buffers may be reused
+  if constexpr (kDeep) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   if constexpr (!kMergeHere) {
     // ---- write this residue's partial; attn_combine merges the eight ----
@@ -596,18 +782,26 @@ __device__ __forceinline__ int rotated_head(const Params& p, int y, int z) {
 
 // Two waves per SIMD (at most 256 registers a wave) up to three row tiles, whatever the workgroup size: the
 // second argument is the minimum waves per SIMD. Four row tiles need more registers and run one wave a SIMD.
+// Decode / verify with one or two row tiles streams two tiles ahead (kDeep): each residue wave walks the
+// sequence's whole context in steps of 8 tiles, long enough for the deeper pipeline to pay (B=16, ctx 4096:
+// 8-10 % faster); three row tiles would spill with it, and the varlen / mixed launch's short decode rows run
+// faster with one tile ahead.
+template <int RT, bool kVarlen>
+constexpr bool deep_decode() { return !kVarlen && RT <= 2; }
+
 template <int RT, bool kVarlen, bool kPaged, int kWaves>
 __global__ __launch_bounds__(kWaves * kWave, RT <= 3 ? 2 : 1) void attn_fwd(Params p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes_rt(kWaves, RT)];
+  constexpr bool kDeep = deep_decode<RT, kVarlen>();
+  __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes_rt(kWaves, RT, kDeep)];
   const int h = rotated_head(p, blockIdx.y, blockIdx.z);
   if constexpr (kVarlen) {
     attn_body<RT, kVarlen, kPaged, kWaves>(p, lds, blockIdx.z, h, blockIdx.x);
   } else {
     // one uniform branch per workgroup between two copies of the body (load policy only)
     if (p.stream_flag == nullptr || *p.stream_flag != 0)
-      attn_body<RT, kVarlen, kPaged, kWaves, 0, true>(p, lds, blockIdx.z, h, blockIdx.x);
+      attn_body<RT, kVarlen, kPaged, kWaves, 0, true, kDeep>(p, lds, blockIdx.z, h, blockIdx.x);
     else
-      attn_body<RT, kVarlen, kPaged, kWaves, 0, false>(p, lds, blockIdx.z, h, blockIdx.x);
+      attn_body<RT, kVarlen, kPaged, kWaves, 0, false, kDeep>(p, lds, blockIdx.z, h, blockIdx.x);
   }
 }
 
