@@ -197,8 +197,9 @@ int sd_verify_drafts(const void* logits, int32_t logits_dtype, int64_t logits_ro
  * nanovllm/layers/embed_head.py:56-68: the logits_indices gather and F.linear) followed by verify_drafts
  * (nanovllm/layers/sampler.py:28-103), as ModelRunner.run_verify calls them (nanovllm/engine/model_runner.py:
  * 482-483). hidden: bf16 [hidden_rows, hidden_dim] rows with row stride hidden_row_stride (16-byte aligned rows);
- * token row m = s*(K+1)+j of the verifier reads hidden row logits_indices[m] (clamped to the table), or row m
- * when logits_indices is NULL. packed_weight: the LM head weight (bf16 [vocab, hidden_dim], rows contiguous) in
+ * token row m = s*(K+1)+j of the verifier reads hidden row logits_indices[m], or row m when logits_indices is
+ * NULL; a sequence with an index outside [0, hidden_rows) gets num_accepted = next_token = -1 (where the
+ * reference's gather raises). packed_weight: the LM head weight (bf16 [vocab, hidden_dim], rows contiguous) in
  * the tile layout sd_lm_head_pack_weight writes, once per model (sd_lm_head_packed_weight_size bytes);
  * hidden_dim a multiple of 32. logits[m, n] = bf16(fp32 sum over hidden_dim) as the library GEMM rounds them.
  * With temperatures == NULL (every row greedy) the logits are never written unless logits_out is given: the

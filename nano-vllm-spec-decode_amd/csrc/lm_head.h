@@ -98,7 +98,8 @@ __global__ __launch_bounds__(256) void lm_head_pack_weight(const uint16_t* __res
   *(u32x4*)(wp + o * 8) = v;
 }
 
-// One thread per 16 bytes of the packed hidden rows (the logits_indices gather, clamped to the table).
+// One thread per 16 bytes of the packed hidden rows (the logits_indices gather; an index outside the table
+// reads nothing and packs a zero row, and lm_head_poison marks its sequence).
 __global__ __launch_bounds__(256) void lm_head_pack_hidden(const uint16_t* __restrict__ hidden, int64_t stride,
                                                            int32_t hidden_rows, const int64_t* __restrict__ rows,
                                                            int32_t M, int32_t Mpad, int32_t H, uint16_t* __restrict__ hp) {
@@ -110,8 +111,8 @@ __global__ __launch_bounds__(256) void lm_head_pack_hidden(const uint16_t* __res
   const int s = (int)(o / (4 * (int64_t)Mpad));
   u32x4 v = {0, 0, 0, 0};
   if (m < M) {
-    const int64_t r = rows ? min(max(rows[m], (int64_t)0), (int64_t)hidden_rows - 1) : (int64_t)m;
-    v = *(const u32x4*)(hidden + r * stride + 32 * s + 8 * c8);
+    const int64_t r = rows ? rows[m] : (int64_t)m;
+    if (r >= 0 && r < hidden_rows) v = *(const u32x4*)(hidden + r * stride + 32 * s + 8 * c8);
   }
   *(u32x4*)(hp + o * 8) = v;
 }

@@ -902,6 +902,23 @@ __global__ __launch_bounds__(64) void lm_head_merge(const lmhead::TileBest* best
   if (threadIdx.x == 0) stats[m] = RowStat{-INFINITY, 0.f, bv, bi};
 }
 
+// A sequence any of whose K+1 rows lists a hidden row outside [0, hidden_rows) gets num_accepted = next_token
+// = -1 (the reference's logits_indices gather raises instead): a bad index never passes as a plausible token.
+__global__ __launch_bounds__(64) void lm_head_poison(const int64_t* rows, int32_t hidden_rows, int32_t S, int32_t K,
+                                                     int64_t* num_accepted, int64_t* next_token) {
+  const int s = blockIdx.x * 64 + threadIdx.x;
+  if (s >= S) return;
+  bool bad = false;
+  for (int j = 0; j <= K; ++j) {
+    const int64_t r = rows[(int64_t)s * (K + 1) + j];
+    bad |= r < 0 || r >= hidden_rows;
+  }
+  if (bad) {
+    num_accepted[s] = -1;
+    next_token[s] = -1;
+  }
+}
+
 int lm_head_mb(int M) { return std::min(lmhead::kMaxMB, std::max(1, ((M + 31) / 32 + 1) / 2)); }
 
 // Token rows of the packed hidden operand: the GEMM grid's rows of workgroups times their rows.
@@ -1174,10 +1191,18 @@ extern "C" int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, 
   int rc = check_launch("lm_head_pack_hidden");
   if (rc) return rc;
   if ((rc = launch_lm_head(a, s))) return rc;
-  if (temperatures)  // sampled rows: the verifier's own passes over the stored logits
-    return run_verify(who, logits_out, SD_DTYPE_BF16, logits_out_row_stride, draft_token_ids, num_drafts, temperatures,
-                      draft_logits, draft_dtype, draft_row_stride, uniforms, exp_noise, S, K, V, num_accepted,
-                      next_token, workspace, workspace_bytes, stream);
+  auto poison = [&]() -> int {
+    if (!logits_indices) return kOk;
+    hipLaunchKernelGGL(lm_head_poison, dim3((unsigned)((S + 63) / 64)), dim3(64), 0, s, logits_indices, hidden_rows, S,
+                       K, num_accepted, next_token);
+    return check_launch("lm_head_poison");
+  };
+  if (temperatures) {  // sampled rows: the verifier's own passes over the stored logits
+    rc = run_verify(who, logits_out, SD_DTYPE_BF16, logits_out_row_stride, draft_token_ids, num_drafts, temperatures,
+                    draft_logits, draft_dtype, draft_row_stride, uniforms, exp_noise, S, K, V, num_accepted,
+                    next_token, workspace, workspace_bytes, stream);
+    return rc ? rc : poison();
+  }
   VParams p{};
   p.logits = logits_out;  // read only for sampled rows (none here)
   p.logits_stride = logits_out_row_stride;
@@ -1195,7 +1220,8 @@ extern "C" int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, 
   hipLaunchKernelGGL(lm_head_merge, dim3((unsigned)M), dim3(64), 0, s, a.best, a.tiles, p.stats);
   if ((rc = check_launch("lm_head_merge"))) return rc;
   hipLaunchKernelGGL((verify_decide<SD_DTYPE_BF16, SD_DTYPE_BF16, false>), dim3(S), dim3(64), 0, s, p);
-  return check_launch("verify_decide");
+  if ((rc = check_launch("verify_decide"))) return rc;
+  return poison();
 }
 
 extern "C" size_t sd_linear_workspace_size(int32_t rows, int32_t out_features, int32_t in_features) {

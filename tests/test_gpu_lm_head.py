@@ -182,3 +182,30 @@ def test_lm_head_mixed_matches_separate_calls(device):
                             torch.zeros(P, device=device))
     ref = lm_head_sample(hidden, head, torch.zeros(D + P, device=device), logits_indices=idx[:D + P])
     assert a.cpu().tolist() == [0] * D and (t.cpu().tolist() + f.cpu().tolist()) == ref.cpu().tolist()
+
+
+def test_lm_head_bad_logits_index_marks_its_sequence(device):
+    """An index outside the hidden rows makes its sequence's accepted count and token -1 (the reference's
+    gather raises); the other sequences are decided as with valid indices, greedy and sampled."""
+    S, K, V, H = 6, 3, 1000, 256
+    N = S * (K + 1) + 4
+    hidden, weight, idx = _inputs(device, 41, S, K, V, H, N=N, gather=True)
+    head = LMHeadVerifier(weight)
+    g = torch.Generator().manual_seed(42)
+    drafts = torch.randint(0, V, (S, K), generator=g).to(device)
+    nd = torch.full((S,), K, dtype=torch.int64, device=device)
+    bad = idx.clone()
+    bad[1 * (K + 1) + 2] = N          # sequence 1: past the table
+    bad[4 * (K + 1)] = -3             # sequence 4: negative
+    for temps in (torch.zeros(S), torch.tensor([0.0, 1.0, 0.5, 0.0, 1.0, 0.7])):
+        u = torch.rand(S, K, generator=g).to(device)
+        e = torch.empty(S, V).exponential_(1, generator=g).to(device)
+        a_ok, t_ok = lm_head_verify(hidden, head, drafts, nd, temps.to(device), logits_indices=idx, uniforms=u,
+                                    exp_noise=e)
+        a, t = lm_head_verify(hidden, head, drafts, nd, temps.to(device), logits_indices=bad, uniforms=u, exp_noise=e)
+        a, t, a_ok, t_ok = a.cpu(), t.cpu(), a_ok.cpu(), t_ok.cpu()
+        for s in range(S):
+            if s in (1, 4):
+                assert a[s] == -1 and t[s] == -1
+            else:
+                assert a[s] == a_ok[s] and t[s] == t_ok[s]

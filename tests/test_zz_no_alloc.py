@@ -75,3 +75,57 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(device):
                                       _lib.stream_of(device))
     assert rc == 2 and b"scratch" in lib.sd_last_error()
     assert ctypes.c_int(rc).value == 2
+
+
+_CAPTURE_SCRIPT = r"""
+import sys, torch
+sys.path[:0] = {paths!r}
+from nanovllm_amd import _lib
+dev = torch.device("cuda:0")
+lib = _lib.load()
+g = torch.Generator().manual_seed(5)
+S, K, V = 32, 4, 151936
+logits = (torch.randn(S * (K + 1), V, generator=g) * 3).to(dev)
+drafts = logits.view(S, K + 1, V)[:, :K].argmax(-1).contiguous()
+drafts[::3, 1] = 7
+nd = torch.full((S,), K, dtype=torch.int64, device=dev)
+temps = torch.tensor([0.0, 1.0] * (S // 2), device=dev)
+u = torch.rand(S, K, generator=g).to(dev)
+e = torch.empty(S, V).exponential_(1, generator=g).to(dev)
+acc = torch.empty(S, dtype=torch.int64, device=dev)
+nxt = torch.empty(S, dtype=torch.int64, device=dev)
+def call(fn, *ws):
+    return fn(logits.data_ptr(), _lib.DTYPE_F32, V, drafts.data_ptr(), nd.data_ptr(), temps.data_ptr(), None, 0, 0,
+              u.data_ptr(), e.data_ptr(), S, K, V, acc.data_ptr(), nxt.data_ptr(), *ws,
+              torch.cuda.current_stream().cuda_stream)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    rc = call(lib.sd_verify_drafts_noalloc)       # the library's first call on this device, under capture
+_lib.check(rc, "sd_verify_drafts_noalloc")
+ws = torch.empty(lib.sd_verify_workspace_size(S, K, V, 0), dtype=torch.uint8, device=dev)
+_lib.check(call(lib.sd_verify_drafts, ws.data_ptr(), ws.numel()), "sd_verify_drafts")
+ref = (acc.cpu().clone(), nxt.cpu().clone())
+for rep in range(3):
+    acc.fill_(-5)
+    nxt.fill_(-5)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert acc.cpu().tolist() == ref[0].tolist() and nxt.cpu().tolist() == ref[1].tolist(), rep
+    torch.randn(1000, device=dev).sum().item()     # the program's own eager work between replays
+print("capture ok", ref[0].tolist()[:8])
+"""
+
+
+def test_noalloc_first_call_under_graph_capture(device):
+    """The entry point's first call on a device happens while a HIP graph is being captured (a fresh process):
+    the scratch address is looked up then, the call is recorded, and three replays, with eager work between
+    them, give what the workspace entry point gives."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    paths = [root, os.path.join(root, "nano-vllm-spec-decode_amd")]
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT.format(paths=paths)], capture_output=True, text=True,
+                         timeout=240)
+    print(res.stdout[-2000:], res.stderr[-2000:], flush=True)
+    assert res.returncode == 0 and "capture ok" in res.stdout
