@@ -69,15 +69,18 @@ def _aliased_cache(device, B, W, Hkv, bs, NB=48, seed=0):
     return kc, vc, tables
 
 
+@pytest.mark.parametrize("W", [1130, 2048])
 @pytest.mark.parametrize("B", [2, 16, 64])
-def test_decode_tables_past_1024_blocks(device, B):
-    """Block size 32 with contexts of 33-36 K keys: tables of 1130 blocks, more than half the 2048 block ids a
-    work item stages in LDS (B = 2: the one-residue stream kernel, 16: four-wave workgroups with partials,
-    64: eight-wave workgroups merging in LDS)."""
-    bs, Hq, Hkv, n, W = 32, 32, 8, 5, 1130
-    kc, vc, tables = _aliased_cache(device, B, W, Hkv, bs, seed=B)
-    rnd = np.random.default_rng(B)
-    ctx = rnd.integers(33000, W * bs + 1, B).tolist()
+def test_decode_tables_past_1024_blocks(device, B, W):
+    """Block size 32 with contexts of 33-36 K keys (tables of 1130 blocks, more than half the 2048 block ids a
+    work item stages in LDS) and up to 65 536 keys (tables of 2048 blocks: the limit, the last context using the
+    last id slot and the last tile of its last block); B = 2: the one-residue stream kernel, 16: four-wave
+    workgroups with partials, 64: eight-wave workgroups merging in LDS."""
+    bs, Hq, Hkv, n = 32, 32, 8, 5
+    kc, vc, tables = _aliased_cache(device, B, W, Hkv, bs, seed=B + W)
+    rnd = np.random.default_rng(B + W)
+    ctx = rnd.integers(W * bs - 3000, W * bs + 1, B).tolist()
+    ctx[0] = W * bs
     q = queries(device, B * n, Hq, D, seed=B + 1).view(B, n, Hq, D)
     lens = torch.tensor(ctx, dtype=torch.int32, device=device)
     out = paged_decode_attention(q, kc, vc, lens, tables, D ** -0.5)
@@ -87,18 +90,20 @@ def test_decode_tables_past_1024_blocks(device, B):
     _check(out.view(B, n, Hq, D)[rows], ref, f"B={B}, tables of {W} blocks")
 
 
-def test_varlen_tables_past_1024_blocks(device):
-    """A 40-query prefill chunk after 34 000 cached keys and a 5-query verify row over 35 000 keys, block size
-    32 (1130-block tables), in one mixed launch and as a prefill-only call."""
-    bs, Hq, Hkv, W = 32, 32, 8, 1130
-    kc, vc, tables = _aliased_cache(device, 2, W, Hkv, bs, seed=7)
-    lq, lk = [5, 40], [35000, 34040]
+@pytest.mark.parametrize("W", [1130, 2048])
+def test_varlen_tables_past_1024_blocks(device, W):
+    """A 40-query prefill chunk after a cached prefix and a 5-query verify row, block size 32, 1130-block tables
+    (34 000 and 35 000 keys) and 2048-block ones (the limit: 65 536 keys for the verify row, its last tile in
+    the last id slot), in one mixed launch and as a prefill-only call."""
+    bs, Hq, Hkv = 32, 32, 8
+    kc, vc, tables = _aliased_cache(device, 2, W, Hkv, bs, seed=7 + W)
+    lq, lk = ([5, 40], [35000, 34040]) if W == 1130 else ([5, 40], [W * bs, W * bs - 1000])
     q = queries(device, sum(lq), Hq, D, seed=8)
     cu_q = torch.tensor([0, 5, 45], dtype=torch.int32, device=device)
     cu_k = torch.tensor([0, lk[0], lk[0] + lk[1]], dtype=torch.int32, device=device)
     out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
     ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
-    _check(out, ref, "varlen, tables of 1130 blocks")
+    _check(out, ref, f"varlen, tables of {W} blocks")
     # the chunk alone (a prefill-only call) gives the same rows bitwise
     cu_q1 = torch.tensor([0, lq[1]], dtype=torch.int32, device=device)
     cu_k1 = torch.tensor([0, lk[1]], dtype=torch.int32, device=device)
