@@ -663,9 +663,14 @@ def cpu_baseline(inputs, min_seconds=10.0, max_reps=8):
         reps += 1
     t = total / reps
     nbytes = decode_bytes(ls.tolist(), q.size(1))
-    return dict(value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(), kind="port",
-                cpu_model=cpu_model(), os_cpu_count=os.cpu_count(),
-                threads_note="16 threads: the host-core share of one GPU on the 8-GPU host, not all cores",
+    threads = torch.get_num_threads()
+    visible = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return dict(value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                cpu_model=cpu_model(), cpu=cpu_info(), os_cpu_count=os.cpu_count(), affinity_cpus=visible,
+                threads_note=(f"{threads} intra-op threads = every one of the {visible} CPUs this process may run "
+                              f"on" if threads >= (visible or 0) else
+                              f"{threads} intra-op threads of the {visible} CPUs this process may run on (capped at "
+                              f"16, the host-CPU share of one GPU)"),
                 sample=f"the full headline call (64 sequences, ctx 4096, k=4) through the oracle's "
                        f"paged_decode_attention, {reps} runs, {total:.1f} s total, {t * 1e3:.0f} ms per call",
                 secondary=cpu_secondary())
@@ -679,6 +684,34 @@ def cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def cpu_info() -> dict:
+    """What /proc/cpuinfo and sysfs say of the first CPU (a virtualised host may report only a bare model name):
+    vendor, family / model / stepping, clock, cache, SIMD extensions the oracle's PyTorch kernels can use, and
+    the NUMA node count."""
+    info = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if not line.strip():
+                break
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+    except OSError:
+        return {}
+    flags = set(info.get("flags", "").split())
+    nodes = [d for d in os.listdir("/sys/devices/system/node") if d.startswith("node")] \
+        if os.path.isdir("/sys/devices/system/node") else []
+    out = {k: info[k] for k in ("vendor_id", "cpu family", "model", "stepping", "cpu MHz", "cache size",
+                                "siblings", "cpu cores") if k in info}
+    out["simd"] = [f for f in ("avx2", "avx512f", "avx512_bf16", "avx512_vnni", "amx_bf16") if f in flags]
+    out["numa_nodes"] = len(nodes)
+    try:
+        import torch
+        out["torch_cpu_capability"] = torch.backends.cpu.get_cpu_capability()
+    except Exception:
+        pass
+    return out
 
 
 def cpu_secondary(reps=3):
