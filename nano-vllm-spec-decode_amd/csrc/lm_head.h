@@ -291,15 +291,18 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
   for (int st = 0; st < 3 && st < nstages; ++st) issue(st);
   handoff(0);
   read_frags(0, 0, a0, b0);
-  for (int s = 0; s < nstages; ++s) {
+  // The last stage is peeled: a loop body without a branch between the hand-off's operand reads and the
+  // second-step MFMAs lets those MFMAs wait only for their own (older) reads, not for the next stage's.
+  for (int s = 0; s + 1 < nstages; ++s) {
     read_frags(s % kRing, 1, a1, b1);
     mfmas(a0, b0);
-    if (s + 1 < nstages) {
-      handoff(s + 1);
-      read_frags((s + 1) % kRing, 0, a0, b0);
-    }
+    handoff(s + 1);
+    read_frags((s + 1) % kRing, 0, a0, b0);
     mfmas(a1, b1);
   }
+  read_frags((nstages - 1) % kRing, 1, a1, b1);
+  mfmas(a0, b0);
+  mfmas(a1, b1);
 
   if (split >= 0) {
     // ---- one range of a split tile: the fp32 sums out, lm_head_fixup finishes the tile ----

@@ -191,11 +191,40 @@ def test_planned_order_bitwise_and_stale_plan(device):
         assert torch.equal(stale, ref), B
 
 
-def test_planned_graph_capture_replays(device):
+@pytest.mark.parametrize("B,n", [(1, 1), (1, 5), (2, 9), (5, 13), (16, 5), (16, 13), (31, 1), (40, 13)])
+def test_planned_few_pairs_equals_unplanned_bitwise(device, B, n):
+    """Few (item, head) pairs (residue partials merged by attn_combine): the planned call (longest first)
+    equals the unplanned one bitwise over several calls on one plan (the layers of a step, each on its own
+    cache), with zero-length and one-key contexts among the sequences (stream kernel: B = 1, 2, 5; four-wave
+    workgroups: B = 16, 31, 40; four row tiles: n = 13)."""
+    from types import SimpleNamespace
+    rnd = random.Random(B * 100 + n)
+    ctx = [rnd.randint(1, 6000) for _ in range(B)]
+    if B > 2:
+        ctx[1], ctx[2] = 0, 1
+    owner = SimpleNamespace()
+    for layer in range(3):
+        kc, vc, tables = paged_cache(device, ctx, 8, 128, W=24, seed=300 + layer)
+        q = queries(device, B * n, 32, 128, seed=301 + layer).view(B, n, 32, 128)
+        lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+        ref = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5)
+        fused = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5, plan_owner=owner)
+        torch.cuda.synchronize()
+        print(f"B={B} n={n} layer {layer}: |out| {fused.float().abs().mean().item():.4f}", flush=True)
+        assert torch.equal(fused, ref), (B, n, layer)
+    if layer == 2 and B == 16 and n == 5:
+        o = oatt.paged_decode_attention(q.cpu(), kc.cpu(), vc.cpu(), lens.cpu(), tables.cpu(), 128 ** -0.5)
+        mx, mean = error_stats(fused.view(B, n, 32, 128), o)
+        assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("B", [32, 8, 1])
+def test_planned_graph_capture_replays(device, B):
     """Attention.forward's decode path (planned) captured at zero lengths, replayed with real metadata: the
-    graph holds the plan and equals the eager result bitwise on every replay."""
+    graph holds the plan and equals the eager result bitwise on every replay (B = 32: residues merged in
+    the workgroup; 8 and 1: partials merged by attn_combine)."""
     from nanovllm_amd.utils.context import Context
-    Hq, Hkv, D, W, n, B = 32, 8, 128, 33, 5, 32
+    Hq, Hkv, D, W, n = 32, 8, 128, 33, 5
     rnd = random.Random(7)
     kc, vc, _ = paged_cache(device, [8192] * B, Hkv, D, W=W, seed=71, extra_blocks=64)
     q = torch.zeros(B, n, Hq, D, dtype=torch.bfloat16, device=device)
