@@ -26,19 +26,19 @@ from nanovllm_amd.engine.metadata import mixed_batch
 from nanovllm_amd.layers.rotary_embedding import qk_norm_rope_store
 
 
-def token_buckets(max_num_batched_tokens: int, step: int = 64) -> list[int]:
+def token_buckets(max_num_batched_tokens: int, step: int = 16) -> list[int]:
     """Total token counts mixed steps are padded to: every `step` up to max_num_batched_tokens (the reference
     uses 64 up to min(budget, 512), model_runner.py:605-615; every kernel here is capturable, so the buckets
-    go up to the whole budget)."""
+    go up to the whole budget). The step is 16 rather than 64: a bucket's padding rows and its work lists'
+    upper bounds cost launch slots in every layer (the 2048-token mixed step of 1164 tokens and 51 requests:
+    1.749 ms replayed in bucket (1216, 64), 1.729 ms in (1168, 56))."""
     return list(range(step, max_num_batched_tokens, step)) + [max_num_batched_tokens]
 
 
-def seq_buckets(max_num_seqs: int) -> list[int]:
-    """Sequence counts (including the padding sequence): powers of two from 2, then max_num_seqs + 1."""
-    out, b = [], 2
-    while b < max_num_seqs + 1:
-        out.append(b)
-        b *= 2
+def seq_buckets(max_num_seqs: int, step: int = 8) -> list[int]:
+    """Sequence counts (including the padding sequence): 2, 4, then every `step`, then max_num_seqs + 1."""
+    out = [b for b in (2, 4) if b < max_num_seqs + 1 and b < step]
+    out += list(range(step, max_num_seqs + 1, step))
     return out + [max_num_seqs + 1]
 
 
@@ -98,7 +98,7 @@ class MixedStepRunner:
 
     def __init__(self, layers, num_heads: int, num_kv_heads: int, head_dim: int, scale: float,
                  block_size: int = 256, max_num_batched_tokens: int = 2048, max_num_seqs: int = 256,
-                 table_width: int = 16, token_step: int = 64, segment=None, device=None, pre_attn=None):
+                 table_width: int = 16, token_step: int = 16, segment=None, device=None, pre_attn=None):
         self.layers = list(layers)
         self.Hq, self.Hkv, self.D, self.scale = num_heads, num_kv_heads, head_dim, scale
         self.block_size, self.W = block_size, table_width

@@ -19,11 +19,15 @@ def seq(tokens, **kw):
 
 
 def test_buckets():
-    assert token_buckets(2048)[:3] == [64, 128, 192] and token_buckets(2048)[-1] == 2048
-    assert len(token_buckets(2048)) == 32
+    assert token_buckets(2048)[:3] == [16, 32, 48] and token_buckets(2048)[-1] == 2048
+    assert len(token_buckets(2048)) == 128
+    assert token_buckets(2048, 64)[:3] == [64, 128, 192] and len(token_buckets(2048, 64)) == 32
     assert token_buckets(100, 64) == [64, 100]
-    assert seq_buckets(256) == [2, 4, 8, 16, 32, 64, 128, 256, 257]
-    assert seq_buckets(1) == [2]
+    assert seq_buckets(256) == [2, 4] + list(range(8, 257, 8)) + [257]
+    assert seq_buckets(64) == [2, 4, 8, 16, 24, 32, 40, 48, 56, 64, 65]
+    assert seq_buckets(63) == [2, 4, 8, 16, 24, 32, 40, 48, 56, 64]
+    assert seq_buckets(7) == [2, 4, 8] and seq_buckets(3) == [2, 4] and seq_buckets(1) == [2]
+    assert seq_buckets(256, 64) == [2, 4, 64, 128, 192, 256, 257]
 
 
 def test_padded_layout_known_answer():
