@@ -280,9 +280,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
                    "+v"(ka[7])
                  :
                  : "memory");
+    // The MFMA runs issue at raised wave priority: a wave with MFMAs ready goes first, so that the other
+    // waves' softmax VALU work fills the matrix core's busy cycles (16 x 1024 prefill 5-7 % faster).
     f32x16 s = f32x16{};
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int st = 0; st < 8; ++st) s = mfma32(ka[st], qv[st], s);
+    __builtin_amdgcn_s_setprio(0);
     const uint32_t vt_addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)vt + v_base;
     u32x2 vr[4][4];
 #pragma unroll
@@ -339,6 +343,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
                    "+v"(vr[3][0]), "+v"(vr[3][1]), "+v"(vr[3][2]), "+v"(vr[3][3])
                  :
                  : "memory");
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
@@ -347,6 +352,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p, uint8_t* lds,
         o[dt] = mfma32(__builtin_bit_cast(bf16x8, w), pb[kk], o[dt]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   // ---- pipeline: stage it in LDS, it+1 and it+2 in registers (ra / rb alternate) ----
