@@ -1,7 +1,7 @@
 // Speculative-decoding verifier and token sampler over the full vocabulary (replaces verify_drafts and
 // Sampler.forward, nanovllm/layers/sampler.py:5-103).
 //
-// Two HBM-streaming kernels over [rows, vocab] tables and two small ones. A row is cut into at most kSpans
+// Two HBM-streaming kernels over [rows, vocab] tables and a small one between them. A row is cut into at most kSpans
 // contiguous spans (a multiple of 4 entries each, none empty); a 256-thread workgroup streams one span with
 // 4-entry loads (16 B for fp32, 8 B for bf16; scalar loads when the rows are not aligned).
 //   1. row_stats       (row, span): first argmax of the raw logits of target rows; for rows with temperature
@@ -17,7 +17,9 @@
 //                      p / max(E, 1e-10) and of residual / max(E, 1e-10) with p = softmax(row a / T), residual =
 //                      max(p - q, 0) (or p with the rejected n-gram guess zeroed), and whether any residual is
 //                      positive; exact values only for the entries that bounds cannot rule out.
-//   3. verify_finish   (seq): random rows only: merges the span candidates and picks the token.
+//                      The last of a sequence's resample workgroups (an arrival count per sequence, zeroed
+//                      by verify_decide; the candidates written and read with the agent-scope cache bit)
+//                      merges the span candidates and picks the token: no launch of its own.
 // Every reduction has a fixed order, so results are deterministic; ties resolve to the first index (and a
 // NaN counts as the largest value), as torch.argmax does.
 #include <math.h>
@@ -240,6 +242,7 @@ struct VParams {
   RowStat* stats;                 // [(S*(K+1) + S*K) rows][nchunk]
   SeqInfo* info;                  // [S]
   Cand* cand;                     // [S][rchunk]
+  int32_t* done;                  // [S]: verify_resample's arrival counters, zeroed by verify_decide (sampled calls)
 };
 
 // One span of one row: the first argmax of the raw values (kArg) and the online (max, sum) of x = value / T
@@ -470,24 +473,38 @@ __global__ __launch_bounds__(64) void verify_decide(VParams p) {
     p.out_a[seq] = a;
     if (!random) p.out_next[seq] = top1[a];
     p.info[seq] = info;
+    if (kRand && p.done) p.done[seq] = 0;
   }
 }
 
-// One workgroup per random sequence: thread k reads span k's candidate (all reads in flight together),
-// then the same block reductions as inside a span. The argmax order (value, then lower index) makes the
-// result independent of the reduction tree. A kernel of its own: merging in the last span workgroup would
-// need device-scope fences (an L2 write-back and invalidate per workgroup on this GPU), which cost more
-// than the launch.
-__global__ __launch_bounds__(kThreads) void verify_finish(VParams p) {
-  __shared__ float shf[4];
-  __shared__ int shi[4];
-  const int seq = blockIdx.x;
-  // The candidates are read with the decision (both in flight together); a greedy sequence has no
-  // candidates (stale workspace), and its workgroup returns before using them.
+// A resample span's candidate, written and read with the agent-scope cache bit (the bit the memory model
+// gives agent-scope atomic stores and loads): coherent across the XCDs' L2s without a fence that writes back
+// or invalidates a whole L2.
+__device__ __forceinline__ void store_cand(Cand* dst, const Cand& c) {
+  __hip_atomic_store((int32_t*)&dst->p_val, __float_as_int(c.p_val), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&dst->p_idx, c.p_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((int32_t*)&dst->r_val, __float_as_int(c.r_val), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&dst->r_idx, c.r_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&dst->any_res, c.any_res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ Cand load_cand(const Cand* src) {
+  Cand c{};
+  c.p_val = __int_as_float(__hip_atomic_load((const int32_t*)&src->p_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  c.p_idx = __hip_atomic_load(&src->p_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  c.r_val = __int_as_float(__hip_atomic_load((const int32_t*)&src->r_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  c.r_idx = __hip_atomic_load(&src->r_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  c.any_res = __hip_atomic_load(&src->any_res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return c;
+}
+
+// The sampled token of a random sequence, by the last of its resample workgroups: thread k reads span k's
+// candidate (all reads in flight together), then the same block reductions as inside a span. The argmax
+// order (value, then lower index) makes the result independent of the reduction tree.
+__device__ __forceinline__ void finish_seq(const VParams& p, int seq, const SeqInfo& info, float* shf, int* shi) {
   float pv = -INFINITY, rv = -INFINITY;
   int pi = 0x7fffffff, ri = 0x7fffffff, any_res = 0;
   for (int k = threadIdx.x; k < p.rchunk; k += kThreads) {
-    const Cand c = p.cand[(int64_t)seq * p.rchunk + k];
+    const Cand c = load_cand(p.cand + (int64_t)seq * p.rchunk + k);
     if (better(c.p_val, c.p_idx, pv, pi)) {
       pv = c.p_val;
       pi = c.p_idx;
@@ -498,8 +515,6 @@ __global__ __launch_bounds__(kThreads) void verify_finish(VParams p) {
     }
     any_res |= c.any_res;
   }
-  const SeqInfo info = p.info[seq];
-  if (!info.random) return;
   block_argmax(pv, pi, shf, shi);
   block_argmax(rv, ri, shf, shi);
   any_res = __syncthreads_or(any_res);
@@ -752,13 +767,23 @@ __global__ __launch_bounds__(kThreads) void verify_resample(VParams p) {
   c.r_val = rv;
   c.r_idx = ri;
   c.any_res = any_res;
-  if (threadIdx.x == 0) p.cand[(int64_t)seq * p.rchunk + chunk] = c;
+  // The span's candidate out, then a count per sequence (zeroed by verify_decide): the sequence's last
+  // workgroup reads every span's candidate and picks the token. No workgroup waits for another.
+  __shared__ int last;
+  if (threadIdx.x == 0) {
+    store_cand(p.cand + (int64_t)seq * p.rchunk + chunk, c);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the candidate is stored before the count
+    const int prev = __hip_atomic_fetch_add(p.done + seq, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == p.rchunk - 1;
+  }
+  __syncthreads();
+  if (last) finish_seq(p, seq, info, shf, shi);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct VLayout {
-  size_t stats, info, cand, total;
+  size_t stats, info, cand, done, total;
 };
 
 // Spans of a row: at most `most`, a multiple of 4 entries each, none empty.
@@ -785,7 +810,8 @@ VLayout verify_layout(int S, int K, int V, bool draft) {
   L.stats = 0;
   L.info = align256((size_t)rows * nchunk * sizeof(RowStat));
   L.cand = align256(L.info + (size_t)S * sizeof(SeqInfo));
-  L.total = align256(L.cand + (size_t)S * rchunk * sizeof(Cand));
+  L.done = align256(L.cand + (size_t)S * rchunk * sizeof(Cand));
+  L.total = align256(L.done + (size_t)S * sizeof(int32_t));
   return L;
 }
 
@@ -806,9 +832,7 @@ int launch_all(const VParams& p, hipStream_t s, bool draft) {
   hipLaunchKernelGGL((verify_decide<DT, DDT, true>), dim3(p.S), dim3(64), 0, s, p);
   if ((rc = check_launch("verify_decide"))) return rc;
   hipLaunchKernelGGL((verify_resample<DT, DDT, kVec>), dim3(p.S, p.rchunk), dim3(kThreads), 0, s, p);
-  if ((rc = check_launch("verify_resample"))) return rc;
-  hipLaunchKernelGGL(verify_finish, dim3(p.S), dim3(kThreads), 0, s, p);
-  return check_launch("verify_finish");
+  return check_launch("verify_resample");
 }
 
 int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
@@ -853,6 +877,7 @@ int run_verify(const char* who, const void* logits, int32_t logits_dtype, int64_
   p.stats = (RowStat*)((uint8_t*)workspace + lay.stats);
   p.info = (SeqInfo*)((uint8_t*)workspace + lay.info);
   p.cand = (Cand*)((uint8_t*)workspace + lay.cand);
+  p.done = (int32_t*)((uint8_t*)workspace + lay.done);
   hipStream_t s = (hipStream_t)stream;
   const bool lf = logits_dtype == SD_DTYPE_F32;
   const bool df = draft && draft_dtype == SD_DTYPE_F32;
