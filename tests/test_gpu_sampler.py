@@ -285,3 +285,49 @@ def test_sampler_matches_oracle(device):
     assert torch.equal(got, ref)
     got16 = Sampler()(logits.to(torch.bfloat16).to(device), temps.to(device), e.to(device)).cpu()
     assert torch.equal(got16, osmp.sample(logits.to(torch.bfloat16), temps, e))
+
+
+def test_verify_graph_replays_equal_eager(device):
+    """verify_drafts captured in a HIP graph (T = 0, 1, 0.7 rows, draft logits, injected noise; the last
+    resample workgroup of each sampled sequence picks its token on counters verify_decide zeroes) and replayed
+    with new inputs and eager calls of another size in between: every replay equals the eager call on the same
+    inputs."""
+    S, K, V = 48, 4, 151936
+    g = torch.Generator(device=device).manual_seed(21)
+    logits = torch.empty(S * (K + 1), V, device=device)
+    dl = torch.empty(S * K, V, device=device)
+    drafts = torch.empty(S, K, dtype=torch.int64, device=device)
+    nd = torch.empty(S, dtype=torch.int64, device=device)
+    temps = torch.tensor([0.0, 1.0, 0.7] * (S // 3), device=device)
+    u = torch.empty(S, K, device=device)
+    e = torch.empty(S, V, device=device)
+
+    def refill(seed):
+        gg = torch.Generator(device=device).manual_seed(seed)
+        logits.copy_(torch.randn(logits.shape, device=device, generator=gg) * 3)
+        dl.copy_(logits.view(S, K + 1, V)[:, :K].reshape(S * K, V) + torch.randn(dl.shape, device=device, generator=gg))
+        top = logits.view(S, K + 1, V)[:, :K].argmax(-1)
+        drafts.copy_(torch.where(torch.rand(S, K, device=device, generator=gg) < 0.6, top,
+                                 torch.randint(0, V, (S, K), device=device, generator=gg)))
+        nd.copy_(torch.randint(0, K + 1, (S,), device=device, generator=gg))
+        u.copy_(torch.rand(S, K, device=device, generator=gg))
+        e.copy_(torch.empty(S, V, device=device).exponential_(1, generator=gg))
+
+    refill(0)
+    verify_drafts(logits, drafts, nd, temps, dl, uniforms=u, exp_noise=e)   # warm-up (workspace)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        acc, nxt = verify_drafts(logits, drafts, nd, temps, dl, uniforms=u, exp_noise=e)
+    small = torch.randn(3 * (K + 1), V, generator=g, device=device)
+    for rep in range(3):
+        refill(100 + rep)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (acc.clone(), nxt.clone())
+        a0, t0 = verify_drafts(logits, drafts, nd, temps, dl, uniforms=u, exp_noise=e)
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], a0) and torch.equal(got[1], t0), rep
+        assert (t0 >= 0).all() and (t0 < V).all()
+        # an eager call of another size on the same workspace between replays
+        verify_drafts(small, drafts[:3], nd[:3], temps[:3], dl[:3 * K], uniforms=u[:3], exp_noise=e[:3])
