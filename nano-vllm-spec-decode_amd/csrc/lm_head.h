@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
   }
   // Every workgroup walks its stages in order from s_begin, so the workgroups of a round read the same hidden
   // stage at about the same time, and the weight, read once, streams with the non-temporal policy: both keep
-  // the hidden rows in L2 (FETCH_SIZE 2.39 -> 1.65 GB per call against rotated starts and default loads, and
+  // the hidden rows in L2 (FETCH_SIZE 2.39 -> 1.28 GB per call against rotated starts and default loads, and
   // 455 -> 443 us).
   auto issue = [&](int st) {
     uint8_t* ring = lds + (st % kRing) * kStageBytes;
