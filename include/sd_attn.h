@@ -8,6 +8,9 @@
  * shape arguments only (not of device-resident lengths), so they can be captured
  * into a hipGraph. All return 0 on success and a non-zero SD_STATUS_* code
  * otherwise; sd_last_error() describes the last failure on the calling thread.
+ * A workspace holds one call's intermediate data (and, for the planned entry
+ * points, the plan): calls that use one workspace must run in one stream's order,
+ * never overlapped.
  *
  * Layouts (row-major, element strides):
  *   KV cache    [num_blocks, block_size, num_kv_heads, head_dim] bf16, one tensor for K and one for V
