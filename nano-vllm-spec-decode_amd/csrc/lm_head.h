@@ -68,7 +68,8 @@ struct Args {
   // `part` ([row of workgroups][tile - full][split][8 waves][2][MB][16][64 lanes]) and lm_head_fixup adds the
   // ranges in order and runs the epilogue. splits = 1: every tile whole (full = tiles). full and splits are
   // functions of (V, H) only and every row of workgroups uses them, so a token row's logits do not depend on
-  // how many rows the call has.
+  // how many rows the call has. The sequential form (lm_head_gemm<MB, true>) runs a split tile's ranges one
+  // after another in one workgroup and adds them in the same order in registers: the same sums, no `part`.
   int32_t full;
   int32_t splits;
   float* part;
@@ -188,9 +189,10 @@ __device__ __forceinline__ void reduce_best(const Args& a, const TileBest* red, 
   }
 }
 
-template <int MB>
+template <int MB, bool kSeq = false>
 __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
   static_assert(MB >= 1 && MB <= kMaxMB, "token blocks per wave");
+  static_assert(!kSeq || MB <= 2, "the sequential ranges keep a second accumulator set");
   constexpr int kRows = 2 * MB * 32;               // token rows of this workgroup
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
   const int tid = threadIdx.x;
@@ -200,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
   // This workgroup's tile and range of H stages (the whole of H, or one range of a split tile).
   const int S = a.H / kK;
   int tile = blockIdx.x, split = -1, s_begin = 0, nstages = S;
-  if ((int)blockIdx.x >= a.full) {
+  if (!kSeq && (int)blockIdx.x >= a.full) {
     const int j = blockIdx.x - a.full;
     tile = a.full + j / a.splits;
     split = j % a.splits;
@@ -287,6 +289,23 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
     asm volatile("" ::: "memory");
     if (next + 3 < nstages) issue(next + 3);
   };
+  // The sequential form: a split tile's range r covers stages r S / splits .. (r + 1) S / splits - 1 (the
+  // physical split's ranges); each is summed from zero, and the ranges are added in order into `sum`, as
+  // lm_head_fixup adds them.
+  const int nranges = kSeq && tile >= a.full ? a.splits : 1;
+  int range = 0, range_end = S / nranges;
+  f32x16 sum[2][kSeq ? MB : 1];
+  auto fold = [&]() {
+    if constexpr (kSeq) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          sum[nb][mb] = range == 0 ? acc[nb][mb] : sum[nb][mb] + acc[nb][mb];
+          acc[nb][mb] = f32x16{};
+        }
+    }
+  };
   bf16x8 a0[2], b0[MB], a1[2], b1[MB];
   for (int st = 0; st < 3 && st < nstages; ++st) issue(st);
   handoff(0);
@@ -299,10 +318,25 @@ __global__ __launch_bounds__(kThreads) void lm_head_gemm(Args a) {
     handoff(s + 1);
     read_frags((s + 1) % kRing, 0, a0, b0);
     mfmas(a1, b1);
+    if constexpr (kSeq) {
+      if (s + 1 == range_end) {  // stage s ends range `range` (registers only: no memory operation)
+        fold();
+        ++range;
+        range_end = (range + 1) * S / nranges;
+      }
+    }
   }
   read_frags((nstages - 1) % kRing, 1, a1, b1);
   mfmas(a0, b0);
   mfmas(a1, b1);
+  if constexpr (kSeq) {
+    if (nranges > 1) {  // the last range, added last
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = sum[nb][mb] + acc[nb][mb];
+    }
+  }
 
   if (split >= 0) {
     // ---- one range of a split tile: the fp32 sums out, lm_head_fixup finishes the tile ----

@@ -995,21 +995,31 @@ LmLayout lm_layout(int S, int K, int V, int H) {
   return L;
 }
 
-// Workspace of sd_linear: the packed rows, then the split tiles' fp32 sums.
+// sd_linear past one row of 320-row workgroups, with split tiles, runs each split tile's ranges one after
+// another in one 128-row workgroup (lm_head_gemm<2, true>): the grid's rows of workgroups already fill the GPU,
+// and the ranges' sums stay in registers instead of going through memory and lm_head_fixup. The sums and their
+// order are the split's, so a row's outputs are the same in both forms.
+constexpr int kSeqMB = 2;
+bool lin_sequential(int M, int N, int K) { return M > 2 * lmhead::kMaxMB * 32 && lm_head_split(N, K).splits > 1; }
+
+// Workspace of sd_linear: the packed rows, then the split tiles' fp32 sums (the physical split only).
 struct LinLayout {
   size_t hp, part, total;
+  int64_t mpad;  // token rows of the packed operand
 };
 LinLayout lin_layout(int M, int N, int K) {
   const int tiles = (N + lmhead::kN - 1) / lmhead::kN;
   const LmSplit sp = lm_head_split(N, K);
+  const bool seq = lin_sequential(M, N, K);
   const int MB = lm_head_mb(M);
-  const int64_t grid_rows = lm_head_mpad(M) / (64 * MB);
   LinLayout L;
+  L.mpad = seq ? ((int64_t)M + 64 * kSeqMB - 1) / (64 * kSeqMB) * (64 * kSeqMB) : lm_head_mpad(M);
+  const int64_t grid_rows = L.mpad / (64 * MB);
   L.hp = 0;
-  L.part = align256((size_t)lm_head_mpad(M) * K * 2);
-  L.total = align256(L.part + (sp.splits > 1 ? (size_t)grid_rows * (tiles - sp.full) * sp.splits * lmhead::kWaves *
-                                                   2 * MB * 16 * kWave * sizeof(float)
-                                             : 0));
+  L.part = align256((size_t)L.mpad * K * 2);
+  L.total = align256(L.part + (sp.splits > 1 && !seq ? (size_t)grid_rows * (tiles - sp.full) * sp.splits *
+                                                           lmhead::kWaves * 2 * MB * 16 * kWave * sizeof(float)
+                                                     : 0));
   return L;
 }
 
@@ -1273,7 +1283,7 @@ extern "C" int sd_linear(const void* x, int64_t x_row_stride, int32_t rows, cons
     return fail(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", who, workspace_bytes, lay.total);
   hipStream_t s = (hipStream_t)stream;
   lmhead::Args a{};
-  a.Mpad = (int32_t)lm_head_mpad(M);
+  a.Mpad = (int32_t)lay.mpad;
   a.hp = (const uint16_t*)((uint8_t*)workspace + lay.hp);
   a.M = M;
   a.wp = (const uint16_t*)packed_weight;
@@ -1293,5 +1303,10 @@ extern "C" int sd_linear(const void* x, int64_t x_row_stride, int32_t rows, cons
                      (const uint16_t*)x, x_row_stride, M, (const int64_t*)nullptr, a.M, a.Mpad, K, (uint16_t*)a.hp);
   const int rc = check_launch("lm_head_pack_hidden");
   if (rc) return rc;
+  if (lin_sequential(M, N, K)) {
+    hipLaunchKernelGGL((lmhead::lm_head_gemm<kSeqMB, true>), dim3((unsigned)a.tiles, (unsigned)(a.Mpad / (64 * kSeqMB))),
+                       dim3(lmhead::kThreads), 0, s, a);
+    return check_launch("lm_head_gemm");
+  }
   return launch_lm_head(a, s);
 }

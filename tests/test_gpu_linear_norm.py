@@ -37,7 +37,8 @@ def _check_rows(x, w, y, rows):
     assert worst <= 1.0 and exact >= 0.999
 
 
-@pytest.mark.parametrize("M,N,K", [(5, 1000, 256), (70, 2053, 192), (330, 6144, 4096), (64, 4096, 12288)])
+@pytest.mark.parametrize("M,N,K", [(5, 1000, 256), (70, 2053, 192), (330, 6144, 4096), (64, 4096, 12288),
+                                   (1300, 4096, 12288)])
 def test_linear_vs_float64(device, M, N, K):
     g = torch.Generator(device=device).manual_seed(M + N)
     x = torch.randn(M, K, device=device, generator=g).to(torch.bfloat16)
@@ -51,10 +52,13 @@ def test_linear_rows_independent_of_row_count(device, name, K, N):
     g = torch.Generator(device=device).manual_seed(K + N)
     x = torch.randn(2048, K, device=device, generator=g).to(torch.bfloat16)
     lin = RowInvariantLinear((torch.randn(N, K, device=device, generator=g) * K ** -0.5).to(torch.bfloat16))
-    first = lin(x[:1])
+    probes = [0, 1, 63, 127, 128, 319, 320, 1000, 1215, 2047]
+    alone = {r: lin(x[r:r + 1]) for r in probes}    # each row in a call of its own
     for M in (2, 16, 64, 80, 320, 325, 1216, 2048):
         y = lin(x[:M])
-        assert torch.equal(y[:1], first), f"{name}: row 0 differs at {M} rows"
+        for r in probes:
+            if r < M:
+                assert torch.equal(y[r:r + 1], alone[r]), f"{name}: row {r} differs at {M} rows"
     # a strided input (a column slice of a wider buffer) gives the same rows
     wide = torch.zeros(64, K + 64, dtype=torch.bfloat16, device=device)
     wide[:, :K] = x[:64]
