@@ -38,7 +38,7 @@ def _check_rows(x, w, y, rows):
 
 
 @pytest.mark.parametrize("M,N,K", [(5, 1000, 256), (70, 2053, 192), (330, 6144, 4096), (64, 4096, 12288),
-                                   (1300, 4096, 12288)])
+                                   (1300, 4096, 12288), (700, 2053, 192)])
 def test_linear_vs_float64(device, M, N, K):
     g = torch.Generator(device=device).manual_seed(M + N)
     x = torch.randn(M, K, device=device, generator=g).to(torch.bfloat16)
