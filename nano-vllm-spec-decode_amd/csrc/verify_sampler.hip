@@ -995,12 +995,17 @@ LmLayout lm_layout(int S, int K, int V, int H) {
   return L;
 }
 
-// sd_linear past one row of 320-row workgroups, with split tiles, runs each split tile's ranges one after
-// another in one 128-row workgroup (lm_head_gemm<2, true>): the grid's rows of workgroups already fill the GPU,
-// and the ranges' sums stay in registers instead of going through memory and lm_head_fixup. The sums and their
-// order are the split's, so a row's outputs are the same in both forms.
+// sd_linear past one row of 320-row workgroups, when every tile is split (fewer tiles than half the CUs: the
+// model's projections), runs each tile's ranges one after another in one 128-row workgroup
+// (lm_head_gemm<2, true>): the grid's rows of workgroups already fill the GPU, and the ranges' sums stay in
+// registers instead of going through memory and lm_head_fixup. The sums and their order are the split's, so a
+// row's outputs are the same in both forms. (With whole tiles too, as at vocabulary sizes, the 320-row
+// workgroups read the weight fewer times and keep the physical split.)
 constexpr int kSeqMB = 2;
-bool lin_sequential(int M, int N, int K) { return M > 2 * lmhead::kMaxMB * 32 && lm_head_split(N, K).splits > 1; }
+bool lin_sequential(int M, int N, int K) {
+  const LmSplit sp = lm_head_split(N, K);
+  return M > 2 * lmhead::kMaxMB * 32 && sp.splits > 1 && sp.full == 0;
+}
 
 // Workspace of sd_linear: the packed rows, then the split tiles' fp32 sums (the physical split only).
 struct LinLayout {

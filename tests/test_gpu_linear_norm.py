@@ -47,7 +47,8 @@ def test_linear_vs_float64(device, M, N, K):
     _check_rows(x, w, y, list(range(0, M, max(1, M // 6))) + [M - 1])
 
 
-@pytest.mark.parametrize("name,K,N", QWEN3_8B)
+# 300 tiles: 256 whole ones and a split last round (the physical split at every row count, as the LM head)
+@pytest.mark.parametrize("name,K,N", QWEN3_8B + [("partly_split", 128, 76800)])
 def test_linear_rows_independent_of_row_count(device, name, K, N):
     g = torch.Generator(device=device).manual_seed(K + N)
     x = torch.randn(2048, K, device=device, generator=g).to(torch.bfloat16)
