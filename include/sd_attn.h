@@ -235,7 +235,9 @@ int sd_lm_head_verify(const void* hidden, int64_t hidden_row_stride, int32_t hid
  * with 16-byte aligned rows (row stride a multiple of 8 elements), out bf16 with any row stride >= out_features. Each output row depends on its
  * input row and the weight only, never on `rows`: the library GEMM picks kernels (and summation orders) by the
  * row count, which changes a model's greedy tokens with the batch; reference counterpart of the property:
- * scripts/check_padding.py:46-52 (GEMMs, padded vs alone).
+ * scripts/check_padding.py:46-52 (GEMMs, padded vs alone). The workspace size is not monotonic in `rows` (a
+ * call of at most 320 rows may hold fp32 range sums that a longer call keeps in registers): size it for each
+ * row count a caller uses.
  */
 size_t sd_linear_workspace_size(int32_t rows, int32_t out_features, int32_t in_features);
 int sd_linear(const void* x, int64_t x_row_stride, int32_t rows, const void* packed_weight, int32_t out_features,
