@@ -12,7 +12,7 @@ import torch
 
 from nanovllm_amd.layers.attention import paged_decode_attention
 from oracle import attention as oatt
-from attn_cases import error_stats, paged_cache, queries
+from attn_cases import error_stats, paged_cache, queries, sub_cache
 
 pytestmark = pytest.mark.gpu
 
@@ -216,6 +216,30 @@ def test_planned_few_pairs_equals_unplanned_bitwise(device, B, n):
         o = oatt.paged_decode_attention(q.cpu(), kc.cpu(), vc.cpu(), lens.cpu(), tables.cpu(), 128 ** -0.5)
         mx, mean = error_stats(fused.view(B, n, 32, 128), o)
         assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+
+
+def test_planned_past_1024_sequences(device):
+    """1100 sequences, more than the plan's 1024-thread sort (the dispatch order is then the index order, and
+    the plan's scan takes two passes): the planned call equals the unplanned one bitwise, and a sample of
+    sequences on both sides of index 1024 (one of them with no context) matches the oracle."""
+    from types import SimpleNamespace
+    B, n = 1100, 5
+    rnd = random.Random(1100)
+    ctx = [rnd.randint(n, 700) for _ in range(B)]
+    ctx[3] = 0
+    kc, vc, tables = paged_cache(device, ctx, 8, 128, seed=77)
+    q = queries(device, B * n, 32, 128, seed=78).view(B, n, 32, 128)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=device)
+    ref = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5)
+    planned = paged_decode_attention(q, kc, vc, lens, tables, 128 ** -0.5, plan_owner=SimpleNamespace())
+    torch.cuda.synchronize()
+    assert torch.equal(planned, ref)
+    sample = [0, 3, 511, 1023, 1024, 1099]
+    skc, svc, st = sub_cache(kc, vc, tables, sample)
+    o = oatt.paged_decode_attention(q[sample].cpu(), skc, svc, lens[sample].cpu(), st, 128 ** -0.5)
+    mx, mean = error_stats(planned.view(B, n, 32, 128)[sample], o)
+    print(f"B={B}: sample max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
 
 
 @pytest.mark.parametrize("B", [32, 8, 1])

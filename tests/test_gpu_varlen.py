@@ -11,7 +11,7 @@ import torch
 from nanovllm_amd.engine.synthetic import mixed_step_lengths as mixed_step
 from nanovllm_amd.layers.attention import paged_decode_attention, varlen_attention
 from oracle import attention as oatt
-from attn_cases import BLOCK, error_stats, paged_cache, queries
+from attn_cases import BLOCK, error_stats, paged_cache, queries, sub_cache
 
 pytestmark = pytest.mark.gpu
 
@@ -100,6 +100,37 @@ def test_random_varlen_batches(device):
         out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
         ref = oatt.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q.cpu(), cu_k.cpu(), D ** -0.5, tables.cpu())
         _check(out, ref, f"random batch {trial}")
+
+
+def test_plan_past_1024_sequences(device):
+    """1100 sequences, more than the plan's 1024-thread sort (work lists in index order, built in two scan
+    passes): verify rows, single decode rows and three prefill chunks after cached keys in one mixed launch.
+    A sample on both sides of index 1024 against the oracle, and the first 1000 sequences' rows bitwise equal
+    to a call with those 1000 alone (sorted dispatch order): the order only changes which workgroup computes
+    an item."""
+    Hq, Hkv, D = 32, 8, 128
+    rnd = np.random.default_rng(5)
+    B = 1100
+    lq = rnd.choice([1, 5, 5, 5], B).tolist()
+    for i in (7, 512, 1050):
+        lq[i] = 40
+    lk = [a + int(rnd.integers(0, 300)) for a in lq]
+    kc, vc, tables = paged_cache(device, lk, Hkv, D, seed=41)
+    q = queries(device, sum(lq), Hq, D, seed=42)
+    cu_q, cu_k = _cu(lq, device), _cu(lk, device)
+    out = varlen_attention(q, kc, vc, cu_q, cu_k, max(lq), max(lk), D ** -0.5, tables)
+    first = 1000
+    r1 = int(cu_q[first])
+    alone = varlen_attention(q[:r1], kc, vc, cu_q[:first + 1], cu_k[:first + 1], max(lq[:first]), max(lk[:first]),
+                             D ** -0.5, tables[:first])
+    torch.cuda.synchronize()
+    assert torch.equal(alone, out[:r1])
+    cq = cu_q.cpu().tolist()
+    for s in (0, 7, 512, 1023, 1024, 1050, 1099):
+        skc, svc, st = sub_cache(kc, vc, tables, [s])
+        ref = oatt.varlen_attention(q[cq[s]:cq[s + 1]].cpu(), skc, svc, torch.tensor([0, lq[s]]), torch.tensor([0, lk[s]]),
+                                    D ** -0.5, st)
+        _check(out[cq[s]:cq[s + 1]], ref, f"sequence {s}: {lq[s]} queries, {lk[s]} keys")
 
 
 def test_prefill_rows_chunk_invariant_bitwise(device):
