@@ -4,7 +4,7 @@ Runs the reference's own nanovllm/layers/sampler.py (loaded on its own from /roo
 it imports only torch) on seeded inputs. Its two internal random draws, torch.rand(S, K) and
 exponential_(1) on an [S, V] tensor, are replaced for the duration of the call by tensors stored in the
 fixture, so any implementation given the same uniforms / noise must return the same accepted counts and
-tokens. Only this container has /root/reference; the GPU box and the tests read the .npz alone.
+tokens. The reference is only read where this script runs; the tests read the .npz alone.
 
     python tests/golden/make_verify_vectors.py
 """
