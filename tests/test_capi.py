@@ -55,6 +55,13 @@ def test_workspace_sizes(lib):
     assert lib.sd_varlen_workspace_size(51, 2048, 4096, 32, 8, 128) > 0
     # per-row statistics of 6 spans (16 B each) for 64 x 5 target and 64 x 4 draft rows
     assert lib.sd_verify_workspace_size(64, 4, 151936, 1) >= (64 * 5 + 64 * 4) * 6 * 16
+    # sd_linear, qkv shape (24 tiles, each split into 8 ranges): up to 320 rows the packed rows plus every
+    # range's fp32 sums (one row of workgroups: 24 x 8 x 327,680 B); past it the ranges run in order in one
+    # workgroup, so only the packed rows (1168 -> 1280 rows of 4096 bf16); not monotonic in the rows
+    small, large = lib.sd_linear_workspace_size(320, 6144, 4096), lib.sd_linear_workspace_size(1168, 6144, 4096)
+    assert small >= 320 * 4096 * 2 + 24 * 8 * 327680 and large == 1280 * 4096 * 2 and large < small
+    # a vocabulary-sized projection keeps the physical split at any row count: sums for every row of workgroups
+    assert lib.sd_linear_workspace_size(640, 151936, 4096) >= 640 * 4096 * 2 + 2 * 82 * 3 * 327680
 
 
 def test_bad_arguments_return_status(lib):
